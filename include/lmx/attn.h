@@ -1,0 +1,195 @@
+/*
+ * lmx/attn.h -- C ABI of the MI355X (gfx950) attention hot path for llmoxide.
+ *
+ * One shared library, libllmoxide_amd.so, exports exactly the functions below.
+ * They replace the wgpu dispatches that llmoxide's crates/gpu records for
+ * attention, KV append and the gated delta rule; each declaration cites the
+ * reference code it stands in for (paths relative to the llmoxide tree).
+ *
+ * Conventions (all entry points):
+ *  - Plain C types only.  Device pointers are caller-owned HIP allocations;
+ *    no entry point allocates, frees or synchronizes the host.  Work is
+ *    enqueued on `stream` (a hipStream_t; NULL = the null stream) and is
+ *    complete when that stream is.
+ *  - Parameters are validated on the host before anything is enqueued.  A
+ *    rejected call returns an LMX_E_* code and enqueues nothing.  No C++
+ *    exception crosses the ABI.
+ *  - Reentrant and thread-compatible: concurrent calls need distinct
+ *    workspaces; one stream per caller thread mirrors the reference's
+ *    Send + !Sync backend (llmoxide/src/backend.rs:57-62).
+ *  - Layouts follow the reference buffers:
+ *      q    [n_tokens, n_heads, head_dim]          (f32 or f16)
+ *      out  [n_tokens, n_heads, head_dim]          f32
+ *      K/V cache rows [n_slots, kv_dim], row = slot(pos)  (f16)
+ *    kv head of query head h is h / (n_heads / n_kv_heads)  (attn.wgsl:78-80).
+ */
+#ifndef LMX_ATTN_H
+#define LMX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Binary-compatible with hipStream_t (typedef struct ihipStream_t*). */
+typedef struct ihipStream_t *lmx_stream;
+
+typedef enum {
+    LMX_OK = 0,
+    LMX_E_NULL = 1,           /* a required pointer is NULL                     */
+    LMX_E_SHAPE = 2,          /* inconsistent or out-of-range geometry          */
+    LMX_E_UNSUPPORTED = 3,    /* valid but not implemented (dtype, head_dim)    */
+    LMX_E_WORKSPACE = 4,      /* workspace missing or too small                 */
+    LMX_E_CONTEXT = 5,        /* positions exceed the cache (ContextOverflow)   */
+    LMX_E_RING_HAZARD = 6,    /* windowed batch would read overwritten slots   */
+    LMX_E_ALIGN = 7,          /* pointer not aligned as the layout requires     */
+    LMX_E_LAUNCH = 8,         /* the HIP runtime rejected a launch              */
+    LMX_E_DEVICE = 9          /* no usable gfx950 device                        */
+} lmx_status;
+
+typedef enum { LMX_F32 = 0, LMX_F16 = 1 } lmx_dtype;
+
+/* The attention uniform, attn.wgsl:22-34 / qwen35.rs:36-49 / forward.rs:29-44,
+ * minus max_vis (a scores-scratch stride this path does not need) and plus
+ * n_slots (rows allocated in each cache buffer, for bounds validation). */
+typedef struct {
+    uint32_t n_tokens;    /* t >= 1, queries at base_pos .. base_pos+t-1      */
+    uint32_t n_heads;     /* H, a multiple of n_kv_heads                      */
+    uint32_t n_kv_heads;  /* Hkv                                              */
+    uint32_t head_dim;    /* 64, 128, 256 or 512                              */
+    uint32_t kv_dim;      /* cache row stride in elements, >= Hkv*head_dim    */
+    uint32_t base_pos;    /* position of the batch's first token              */
+    uint32_t window;      /* 0 = global linear cache, else ring of `window`   */
+    uint32_t n_slots;     /* rows in each K/V cache buffer                    */
+    uint32_t bidi;        /* 1 = the batch also attends forward to itself     */
+    float scale;          /* softmax scale, applied verbatim                  */
+} lmx_attn_params;
+
+/* write_cache's view of one append, ops.wgsl:323-346 (Op{n_rows, dim, u0, u1}). */
+typedef struct {
+    uint32_t n_tokens;    /* rows to append                                   */
+    uint32_t kv_dim;      /* elements per row                                 */
+    uint32_t base_pos;    /* position of row 0                                */
+    uint32_t window;      /* 0 = linear, else ring: slot = pos % window       */
+    uint32_t n_slots;     /* rows allocated in the cache                      */
+} lmx_kv_desc;
+
+/* The delta-net uniform, deltanet.wgsl:20-34 / qwen35.rs:51-68, restricted to
+ * what the recurrence reads.  Conv taps and the conv window belong to the
+ * prologue kernels, which stay outside this library. */
+typedef struct {
+    uint32_t n_tok;       /* tokens in the batch                              */
+    uint32_t conv_dim;    /* row stride of the conv stream, 2*key_dim+d_inner */
+    uint32_t key_dim;     /* n_kh * s_dim                                     */
+    uint32_t d_inner;     /* n_vh * s_dim                                     */
+    uint32_t s_dim;       /* state side; 128 (64 also accepted)               */
+    uint32_t n_vh;        /* value heads                                      */
+    uint32_t n_kh;        /* key heads; v-head hv reads k-head hv % n_kh      */
+    float scale;          /* output scale, 1/sqrt(s_dim) in the reference     */
+} lmx_dop;
+
+/* Human-readable name of a status code (static storage). */
+const char *lmx_status_str(lmx_status s);
+
+/* Library version as 10000*major + 100*minor + patch. */
+int lmx_version(void);
+
+/* Zero a workspace before its first use (a fill kernel, not hipMemsetAsync,
+ * so the call may sit inside a captured graph).  Every entry point leaves the
+ * workspace's counters at zero when its work completes. */
+lmx_status lmx_workspace_init(void *ws, size_t ws_bytes, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * KV append.  Replaces the two `write_cache` dispatches per attention layer:
+ * ops.wgsl:323-346, dispatched at qwen35.rs:1062-1074 and forward.rs:964-985;
+ * CPU semantics LayerCache::store/slot, cache.rs:21-28, 58-62.
+ * Row i of k_new/v_new ([n_tokens, kv_dim] f32) is rounded to f16 (RNE) and
+ * stored at slot(base_pos + i).  When one call maps several rows to the same
+ * ring slot, the latest position wins, as the reference's in-order store does.
+ * Either of k_new/v_new (with its cache) may be NULL to append only the other.
+ */
+lmx_status lmx_kv_append(const lmx_kv_desc *d, const float *k_new, const float *v_new,
+                         void *k_cache, void *v_cache, lmx_dtype cache_dt, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Attention.  Replaces the scores_pass / softmax_pass / weighted_v dispatch
+ * triple (attn.wgsl:84-232) recorded at qwen35.rs:1076-1094 and
+ * forward.rs:988-1011 (and vision.rs:587-631 with bidi=1), computing the CPU
+ * reference's result (cpu.rs:342-387; qwen35/cpu.rs:324-365):
+ *   out[i,h,:] = softmax_p(scale * q[i,h,:] . K[p, h/G, :]) V[p, h/G, :]
+ * over the visible positions p of query pos = base_pos+i:
+ *   lo = window ? max(0, pos-window+1) : 0
+ *   hi = bidi ? (window ? min(base_pos+t-1, pos+window-1) : base_pos+t-1) : pos
+ * K/V for position p are read from cache row slot(p) = window ? p%window : p,
+ * except that positions >= base_pos are read from k_cur/v_cur row p-base_pos
+ * when those are given ([n_tokens, kv_dim] f16).  The reference stores the
+ * batch before attending, so a windowed batch with base_pos+t > window reads
+ * slots that later rows of the same batch overwrote; this call refuses that
+ * case (LMX_E_RING_HAZARD) unless k_cur/v_cur are given.
+ * q_dt: LMX_F32 or LMX_F16.  kv_dt: LMX_F16.
+ * Workspace: lmx_attn_workspace_bytes(p) bytes, zeroed once by
+ * lmx_workspace_init; 0 bytes may be asked for (ws may then be NULL).
+ */
+size_t lmx_attn_workspace_bytes(const lmx_attn_params *p);
+
+lmx_status lmx_attn_fwd(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,
+                        const void *k_cache, const void *v_cache, lmx_dtype kv_dt,
+                        const void *k_cur, const void *v_cur, float *out,
+                        void *ws, size_t ws_bytes, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Ragged multi-sequence decode: one query token per sequence, each sequence
+ * with its own contiguous cache.  The reference serves one sequence at a time
+ * (docs/limitations.md:21); this is the batched form of lmx_attn_fwd with
+ * n_tokens = 1 and, for sequence b, base_pos = ctx_lens[b]-1.  With n_seq = 1
+ * it computes exactly what lmx_attn_fwd does.
+ *   p          geometry; n_tokens must be 1 and base_pos is ignored
+ *   ctx_lens   device int32 [n_seq], each in [1, max_ctx], max_ctx <= n_slots
+ *   k_ptrs     device array [n_seq] of f16 cache pointers (likewise v_ptrs)
+ *   q          [n_seq, n_heads, head_dim];  out [n_seq, n_heads, head_dim] f32
+ */
+size_t lmx_attn_decode_batched_workspace_bytes(const lmx_attn_params *p, int32_t n_seq,
+                                               int32_t max_ctx);
+
+lmx_status lmx_attn_decode_batched(const lmx_attn_params *p, int32_t n_seq, int32_t max_ctx,
+                                   const int32_t *ctx_lens, const void *const *k_ptrs,
+                                   const void *const *v_ptrs, const void *q, lmx_dtype q_dt,
+                                   lmx_dtype kv_dt, float *out, void *ws, size_t ws_bytes,
+                                   lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Gated delta rule, token-sequential.  Replaces `delta_recur`
+ * (deltanet.wgsl:193-239, dispatched at qwen35.rs:960-965); CPU semantics
+ * qwen35/cpu.rs:218-245.  Per token i and v-head hv (k-head hk = hv % n_kh):
+ *   g = exp(ssm_a[hv] * softplus(alpha[i,hv] + dt_bias[hv])), b = sigmoid(beta[i,hv])
+ *   S <- g S;  for each row j: d = b (v_j - S_j . k);  S_j += d k;  o_j = scale S_j . q
+ *   conv   [n_tok, conv_dim] f32, channels q | k | v, q and k L2-normalized
+ *   alpha, beta [n_tok, n_vh] f32;  ssm_a, dt_bias [n_vh] f32
+ *   state  [n_vh, s_dim (row j), s_dim] f32, updated in place
+ *   out    [n_tok, d_inner] f32
+ */
+lmx_status lmx_deltanet_recur(const lmx_dop *op, const float *ssm_a, const float *dt_bias,
+                              const float *alpha, const float *beta, const float *conv,
+                              float *state, float *out, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Gated delta rule, chunked (chunk tokens at a time, WY/UT form).  Same
+ * contract and results as lmx_deltanet_recur within the stated tolerance; the
+ * reference has no chunked form (it runs the token loop in one workgroup per
+ * head, deltanet.wgsl:175-239), so this is the prefill counterpart of the same
+ * dispatch.  chunk: 64 (or 32, 16).
+ */
+size_t lmx_deltanet_chunked_workspace_bytes(const lmx_dop *op, int32_t chunk);
+
+lmx_status lmx_deltanet_chunked(const lmx_dop *op, const float *ssm_a, const float *dt_bias,
+                                const float *alpha, const float *beta, const float *conv,
+                                float *state, float *out, int32_t chunk, void *ws,
+                                size_t ws_bytes, lmx_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LMX_ATTN_H */

@@ -1,0 +1,333 @@
+"""llmoxide_amd -- MI355X (gfx950) attention hot path for llmoxide.
+
+The product is ``libllmoxide_amd.so``, a C-ABI library (``include/lmx/attn.h``)
+of hand-written HIP kernels.  This module is the host-side mirror of the
+reference's dispatch interface for that path, in Python over ``ctypes``:
+
+=========================  ==================================================
+this module                reference dispatch it mirrors
+=========================  ==================================================
+``write_cache``            ``write_cache`` (ops.wgsl:323-346; qwen35.rs:1062-1074)
+``attention``              ``scores_pass``/``softmax_pass``/``weighted_v``
+                           (attn.wgsl:84-232; qwen35.rs:1076-1094,
+                           forward.rs:988-1011)
+``attention_decode_batched``  the same, one query per sequence, ragged
+``delta_recur``            ``delta_recur`` (deltanet.wgsl:193-239;
+                           qwen35.rs:960-965)
+``delta_chunked``          chunked prefill form of ``delta_recur``
+=========================  ==================================================
+
+Tensors are torch tensors on a ROCm device (torch provides device memory and
+streams only).  Every call goes through the C ABI; there is no CPU fallback:
+if the library is missing, :func:`lib` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import math
+import os
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libllmoxide_amd.so")
+
+
+class Status(enum.IntEnum):
+    OK = 0
+    E_NULL = 1
+    E_SHAPE = 2
+    E_UNSUPPORTED = 3
+    E_WORKSPACE = 4
+    E_CONTEXT = 5
+    E_RING_HAZARD = 6
+    E_ALIGN = 7
+    E_LAUNCH = 8
+    E_DEVICE = 9
+
+
+F32, F16 = 0, 1
+
+
+class LmxError(RuntimeError):
+    """A call rejected by the library; ``.status`` is the :class:`Status`."""
+
+    def __init__(self, fn: str, status: int):
+        self.status = Status(status)
+        super().__init__(f"{fn}: {self.status.name} ({lib().lmx_status_str(status).decode()})")
+
+
+class AttnParams(ctypes.Structure):
+    """lmx_attn_params: the reference's ``Attn`` uniform (attn.wgsl:22-34)
+    without ``max_vis``, plus ``n_slots``."""
+    _fields_ = [
+        ("n_tokens", ctypes.c_uint32),
+        ("n_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("kv_dim", ctypes.c_uint32),
+        ("base_pos", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("n_slots", ctypes.c_uint32),
+        ("bidi", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class KvDesc(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", ctypes.c_uint32),
+        ("kv_dim", ctypes.c_uint32),
+        ("base_pos", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("n_slots", ctypes.c_uint32),
+    ]
+
+
+class Dop(ctypes.Structure):
+    """lmx_dop: the reference's ``DOp`` uniform (deltanet.wgsl:20-34), the
+    fields the recurrence reads."""
+    _fields_ = [
+        ("n_tok", ctypes.c_uint32),
+        ("conv_dim", ctypes.c_uint32),
+        ("key_dim", ctypes.c_uint32),
+        ("d_inner", ctypes.c_uint32),
+        ("s_dim", ctypes.c_uint32),
+        ("n_vh", ctypes.c_uint32),
+        ("n_kh", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+# Every symbol include/lmx/attn.h declares, with its ctypes signature.
+_VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
+_PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINTER(Dop)
+SIGNATURES = {
+    "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
+    "lmx_version": (ctypes.c_int, []),
+    "lmx_workspace_init": (ctypes.c_int, [_VP, _SZ, _VP]),
+    "lmx_kv_append": (ctypes.c_int, [_PK, _VP, _VP, _VP, _VP, ctypes.c_int, _VP]),
+    "lmx_attn_workspace_bytes": (_SZ, [_PA]),
+    "lmx_attn_fwd": (ctypes.c_int, [_PA, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP, _VP, _VP,
+                                    _VP, _SZ, _VP]),
+    "lmx_attn_decode_batched_workspace_bytes": (_SZ, [_PA, _I32, _I32]),
+    "lmx_attn_decode_batched": (ctypes.c_int, [_PA, _I32, _I32, _VP, _VP, _VP, _VP, ctypes.c_int,
+                                               ctypes.c_int, _VP, _VP, _SZ, _VP]),
+    "lmx_deltanet_recur": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "lmx_deltanet_chunked_workspace_bytes": (_SZ, [_PD, _I32]),
+    "lmx_deltanet_chunked": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I32, _VP, _SZ,
+                                            _VP]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libllmoxide_amd.so; raise (never fall back) if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m llmoxide_amd.build` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(fn: str, rc: int) -> None:
+    if rc != 0:
+        raise LmxError(fn, rc)
+
+
+# ---------------------------------------------------------------- helpers --
+def _torch():
+    import torch  # deferred: the ABI checks need no torch
+    return torch
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _dt(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float16:
+        return F16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _need_cuda(*ts) -> None:
+    for t in ts:
+        if t is not None and (not t.is_cuda or not t.is_contiguous()):
+            raise ValueError("tensors must be contiguous and on the GPU")
+
+
+class Workspace:
+    """A zero-initialized device scratch buffer shared by successive calls.
+
+    Calls on one Workspace must be ordered on one stream (the library leaves
+    its counters at zero after each call, so no re-clear is needed between
+    calls).  It grows on demand; growth re-allocates and re-clears.
+    """
+
+    def __init__(self, nbytes: int = 0, device=None):
+        self.device = device
+        self.buf = None
+        self.nbytes = 0
+        if nbytes:
+            self.ensure(nbytes)
+
+    def ensure(self, nbytes: int, stream=None):
+        torch = _torch()
+        if nbytes <= self.nbytes:
+            return self
+        nbytes = (nbytes + 255) // 256 * 256
+        self.buf = torch.empty(nbytes + 256, dtype=torch.uint8,
+                               device=self.device or torch.device("cuda"))
+        off = (-self.buf.data_ptr()) % 256
+        self.base = self.buf.data_ptr() + off
+        self.nbytes = nbytes
+        _check("lmx_workspace_init", lib().lmx_workspace_init(self.base, nbytes, _stream(stream)))
+        return self
+
+
+def attn_params(*, n_tokens, n_heads, n_kv_heads, head_dim, base_pos, n_slots, window=0,
+                bidi=False, scale=None, kv_dim=None) -> AttnParams:
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    return AttnParams(n_tokens, n_heads, n_kv_heads, head_dim, kv_dim or n_kv_heads * head_dim,
+                      base_pos, window, n_slots, int(bool(bidi)), scale)
+
+
+# --------------------------------------------------------------- the path --
+def write_cache(k_new, v_new, k_cache, v_cache, *, base_pos: int, window: int = 0, stream=None):
+    """Append f32 rows [t, kv_dim] into f16 caches [n_slots, kv_dim] at
+    slot(base_pos + i) (ops.wgsl:323-346).  Either pair may be None."""
+    _need_cuda(k_new, v_new, k_cache, v_cache)
+    src = k_new if k_new is not None else v_new
+    cache = k_cache if k_cache is not None else v_cache
+    d = KvDesc(src.shape[0], src.shape[-1], base_pos, window, cache.shape[0])
+    rc = lib().lmx_kv_append(ctypes.byref(d), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache),
+                             F16, _stream(stream))
+    _check("lmx_kv_append", rc)
+
+
+def attention(q, k_cache, v_cache, *, n_heads: int, n_kv_heads: int, head_dim: int,
+              base_pos: int, window: int = 0, bidi: bool = False, scale: Optional[float] = None,
+              k_cur=None, v_cur=None, out=None, workspace: Optional[Workspace] = None,
+              kv_dim: Optional[int] = None, stream=None):
+    """GQA attention of q [t, H*hd] (f32/f16) over f16 caches [n_slots, kv_dim].
+
+    Returns out [t, H*hd] f32.  The semantics are the reference's CPU attention
+    (cpu.rs:342-387; qwen35/cpu.rs:324-365); see include/lmx/attn.h.
+    """
+    torch = _torch()
+    _need_cuda(q, k_cache, v_cache, k_cur, v_cur, out)
+    t = q.shape[0]
+    p = attn_params(n_tokens=t, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+                    base_pos=base_pos, n_slots=k_cache.shape[0], window=window, bidi=bidi,
+                    scale=scale, kv_dim=kv_dim)
+    if out is None:
+        out = torch.empty((t, n_heads * head_dim), dtype=torch.float32, device=q.device)
+    need = lib().lmx_attn_workspace_bytes(ctypes.byref(p))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        workspace = workspace or Workspace(device=q.device)
+        workspace.ensure(need, stream)
+        ws_ptr, ws_bytes = workspace.base, workspace.nbytes
+    rc = lib().lmx_attn_fwd(ctypes.byref(p), _ptr(q), _dt(q), _ptr(k_cache), _ptr(v_cache), F16,
+                            _ptr(k_cur), _ptr(v_cur), _ptr(out), ws_ptr, ws_bytes, _stream(stream))
+    _check("lmx_attn_fwd", rc)
+    return out
+
+
+class BatchedCaches:
+    """Device pointer tables for :func:`attention_decode_batched`."""
+
+    def __init__(self, k_caches: Sequence, v_caches: Sequence, device=None):
+        torch = _torch()
+        self.k_caches, self.v_caches = list(k_caches), list(v_caches)
+        dev = device or self.k_caches[0].device
+        self.k_ptrs = torch.tensor([c.data_ptr() for c in self.k_caches], dtype=torch.int64, device=dev)
+        self.v_ptrs = torch.tensor([c.data_ptr() for c in self.v_caches], dtype=torch.int64, device=dev)
+
+
+def attention_decode_batched(q, caches: BatchedCaches, ctx_lens, *, max_ctx: int, n_heads: int,
+                             n_kv_heads: int, head_dim: int, window: int = 0,
+                             scale: Optional[float] = None, n_slots: Optional[int] = None,
+                             out=None, workspace: Optional[Workspace] = None, stream=None):
+    """One query token per sequence: q [B, H*hd], ctx_lens int32 [B] on device."""
+    torch = _torch()
+    _need_cuda(q, ctx_lens, out)
+    B = q.shape[0]
+    p = attn_params(n_tokens=1, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+                    base_pos=0, n_slots=n_slots or caches.k_caches[0].shape[0], window=window,
+                    scale=scale)
+    if out is None:
+        out = torch.empty((B, n_heads * head_dim), dtype=torch.float32, device=q.device)
+    need = lib().lmx_attn_decode_batched_workspace_bytes(ctypes.byref(p), B, max_ctx)
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        workspace = workspace or Workspace(device=q.device)
+        workspace.ensure(need, stream)
+        ws_ptr, ws_bytes = workspace.base, workspace.nbytes
+    rc = lib().lmx_attn_decode_batched(ctypes.byref(p), B, max_ctx, _ptr(ctx_lens),
+                                       _ptr(caches.k_ptrs), _ptr(caches.v_ptrs), _ptr(q), _dt(q), F16,
+                                       _ptr(out), ws_ptr, ws_bytes, _stream(stream))
+    _check("lmx_attn_decode_batched", rc)
+    return out
+
+
+def dop(*, n_tok, n_vh, n_kh, s_dim, scale=None) -> Dop:
+    key_dim, d_inner = n_kh * s_dim, n_vh * s_dim
+    scale = 1.0 / math.sqrt(s_dim) if scale is None else scale
+    return Dop(n_tok, 2 * key_dim + d_inner, key_dim, d_inner, s_dim, n_vh, n_kh, scale)
+
+
+def delta_recur(conv, alpha, beta, state, ssm_a, dt_bias, *, n_vh, n_kh, s_dim, out=None,
+                stream=None):
+    """Token-sequential gated delta rule (deltanet.wgsl:193-239).  ``state``
+    [n_vh, s_dim, s_dim] f32 is updated in place; returns out [t, d_inner]."""
+    torch = _torch()
+    _need_cuda(conv, alpha, beta, state, ssm_a, dt_bias, out)
+    op = dop(n_tok=conv.shape[0], n_vh=n_vh, n_kh=n_kh, s_dim=s_dim)
+    if out is None:
+        out = torch.empty((conv.shape[0], op.d_inner), dtype=torch.float32, device=conv.device)
+    rc = lib().lmx_deltanet_recur(ctypes.byref(op), _ptr(ssm_a), _ptr(dt_bias), _ptr(alpha),
+                                  _ptr(beta), _ptr(conv), _ptr(state), _ptr(out), _stream(stream))
+    _check("lmx_deltanet_recur", rc)
+    return out
+
+
+def delta_chunked(conv, alpha, beta, state, ssm_a, dt_bias, *, n_vh, n_kh, s_dim, chunk=64,
+                  out=None, workspace: Optional[Workspace] = None, stream=None):
+    """Chunked gated delta rule; same contract as :func:`delta_recur`."""
+    torch = _torch()
+    _need_cuda(conv, alpha, beta, state, ssm_a, dt_bias, out)
+    op = dop(n_tok=conv.shape[0], n_vh=n_vh, n_kh=n_kh, s_dim=s_dim)
+    if out is None:
+        out = torch.empty((conv.shape[0], op.d_inner), dtype=torch.float32, device=conv.device)
+    need = lib().lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk)
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        workspace = workspace or Workspace(device=conv.device)
+        workspace.ensure(need, stream)
+        ws_ptr, ws_bytes = workspace.base, workspace.nbytes
+    rc = lib().lmx_deltanet_chunked(ctypes.byref(op), _ptr(ssm_a), _ptr(dt_bias), _ptr(alpha),
+                                    _ptr(beta), _ptr(conv), _ptr(state), _ptr(out), chunk, ws_ptr,
+                                    ws_bytes, _stream(stream))
+    _check("lmx_deltanet_chunked", rc)
+    return out

@@ -1,0 +1,275 @@
+// extern "C" entry points of libllmoxide_amd.so (declared in include/lmx/attn.h).
+//
+// Every entry point validates its arguments on the host before it enqueues
+// anything and reports failures as lmx_status codes, mirroring the reference's
+// host-side checks (ensure! on batch and context, qwen35.rs:1212-1222;
+// forward.rs:1385-1395) and its error enum (llmoxide/src/error.rs:9-47).
+#include <cmath>
+
+#include "common.hpp"
+
+namespace lmx {
+
+// attn_decode.hip
+size_t decode_workspace_bytes(const lmx_attn_params* p);
+size_t decode_batched_workspace_bytes(const lmx_attn_params* p, int n_seq, int max_ctx);
+lmx_status decode_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
+                      const void* v_cache, const void* k_cur, const void* v_cur, float* out,
+                      void* ws, size_t ws_bytes, hipStream_t st);
+lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, const int32_t* ctx_lens,
+                          const void* const* k_ptrs, const void* const* v_ptrs, const void* q,
+                          lmx_dtype q_dt, float* out, void* ws, size_t ws_bytes, hipStream_t st);
+// attn_prefill.hip
+bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt);
+lmx_status prefill_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
+                       const void* v_cache, const void* k_cur, const void* v_cur, float* out,
+                       hipStream_t st);
+// deltanet.hip
+lmx_status deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
+                          const float* alpha, const float* beta, const float* conv, float* state,
+                          float* out, hipStream_t st);
+size_t deltanet_chunked_ws(const lmx_dop* op, int chunk);
+lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
+                            const float* alpha, const float* beta, const float* conv,
+                            float* state, float* out, int chunk, void* ws, size_t ws_bytes,
+                            hipStream_t st);
+
+// Queries with at most this many tokens take the split-K path; longer
+// batches take the MFMA tile path.
+constexpr uint32_t kSplitKMaxTokens = 8;
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+static lmx_status check_attn_params(const lmx_attn_params* p) {
+    if (!p) return LMX_E_NULL;
+    if (p->n_tokens == 0 || p->n_heads == 0 || p->n_kv_heads == 0) return LMX_E_SHAPE;
+    if (p->n_heads % p->n_kv_heads) return LMX_E_SHAPE;
+    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256 && p->head_dim != 512)
+        return LMX_E_UNSUPPORTED;
+    if ((uint64_t)p->kv_dim < (uint64_t)p->n_kv_heads * p->head_dim || p->kv_dim % 8) return LMX_E_SHAPE;
+    if (!std::isfinite(p->scale)) return LMX_E_SHAPE;
+    if (p->bidi > 1) return LMX_E_SHAPE;
+    const uint64_t end = (uint64_t)p->base_pos + p->n_tokens;
+    if (end >= (1ull << 31)) return LMX_E_CONTEXT;
+    if (p->window == 0) {
+        if (end > p->n_slots) return LMX_E_CONTEXT;
+    } else {
+        if (p->n_slots < p->window) return LMX_E_SHAPE;
+    }
+    return LMX_OK;
+}
+
+static bool use_split_k(const lmx_attn_params* p, lmx_dtype q_dt) {
+    return p->n_tokens <= kSplitKMaxTokens || !prefill_supported(p, q_dt);
+}
+
+// Fill kernel for the workspace (a kernel rather than hipMemsetAsync, so it
+// can be recorded into a graph).
+__global__ void zero_words(uint32_t* p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// write_cache (ops.wgsl:323-346): four elements per thread, f32 -> f16 RNE.
+// Row i is skipped when row i + window of the same call maps to the same ring
+// slot, so the latest position wins as in the reference's in-order store.
+__global__ void kv_append_kernel(const float* __restrict__ src, f16* __restrict__ cache,
+                                 uint32_t n_tokens, uint32_t kv_dim, uint32_t base_pos,
+                                 uint32_t window) {
+    const uint32_t per_row = kv_dim / 4;
+    const size_t n = (size_t)n_tokens * per_row;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t row = (uint32_t)(i / per_row);
+        const uint32_t c4 = (uint32_t)(i - (size_t)row * per_row);
+        if (window && row + window < n_tokens) continue;
+        const uint32_t pos = base_pos + row;
+        const uint32_t slot = window ? pos % window : pos;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + (size_t)row * kv_dim + 4 * c4);
+        f16x4 h;
+        h[0] = (f16)x[0];
+        h[1] = (f16)x[1];
+        h[2] = (f16)x[2];
+        h[3] = (f16)x[3];
+        *reinterpret_cast<f16x4*>(cache + (size_t)slot * kv_dim + 4 * c4) = h;
+    }
+}
+
+}  // namespace lmx
+
+using namespace lmx;
+
+extern "C" {
+
+const char* lmx_status_str(lmx_status s) {
+    switch (s) {
+        case LMX_OK: return "ok";
+        case LMX_E_NULL: return "required pointer is NULL";
+        case LMX_E_SHAPE: return "inconsistent or out-of-range geometry";
+        case LMX_E_UNSUPPORTED: return "unsupported dtype or head_dim";
+        case LMX_E_WORKSPACE: return "workspace missing or too small";
+        case LMX_E_CONTEXT: return "positions exceed the cache (context overflow)";
+        case LMX_E_RING_HAZARD: return "windowed batch would read ring slots it overwrites; pass k_cur/v_cur";
+        case LMX_E_ALIGN: return "pointer misaligned for its layout";
+        case LMX_E_LAUNCH: return "HIP launch failed";
+        case LMX_E_DEVICE: return "no usable gfx950 device";
+    }
+    return "unknown status";
+}
+
+int lmx_version(void) { return 100; }
+
+lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
+    if (ws_bytes == 0) return LMX_OK;
+    if (!ws) return LMX_E_NULL;
+    if (!aligned(ws, 4) || ws_bytes % 4) return LMX_E_ALIGN;
+    const size_t n = ws_bytes / 4;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(zero_words, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<uint32_t*>(ws), n);
+    LMX_CHECK_LAUNCH();
+    return LMX_OK;
+}
+
+lmx_status lmx_kv_append(const lmx_kv_desc* d, const float* k_new, const float* v_new,
+                         void* k_cache, void* v_cache, lmx_dtype cache_dt, lmx_stream stream) {
+    if (!d) return LMX_E_NULL;
+    if (cache_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if ((k_new == nullptr) != (k_cache == nullptr) || (v_new == nullptr) != (v_cache == nullptr))
+        return LMX_E_NULL;
+    if (!k_new && !v_new) return LMX_E_NULL;
+    if (d->n_tokens == 0 || d->kv_dim == 0 || d->kv_dim % 4) return LMX_E_SHAPE;
+    const uint64_t end = (uint64_t)d->base_pos + d->n_tokens;
+    if (end >= (1ull << 32)) return LMX_E_CONTEXT;
+    if (d->window == 0) {
+        if (end > d->n_slots) return LMX_E_CONTEXT;
+    } else if (d->n_slots < d->window) {
+        return LMX_E_SHAPE;
+    }
+    for (const void* p : {(const void*)k_new, (const void*)v_new})
+        if (p && !aligned(p, 16)) return LMX_E_ALIGN;
+    for (const void* p : {(const void*)k_cache, (const void*)v_cache})
+        if (p && !aligned(p, 8)) return LMX_E_ALIGN;
+    const size_t n = (size_t)d->n_tokens * (d->kv_dim / 4);
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    (void)hipGetLastError();
+    if (k_new)
+        hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           k_new, static_cast<f16*>(k_cache), d->n_tokens, d->kv_dim, d->base_pos,
+                           d->window);
+    if (v_new)
+        hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           v_new, static_cast<f16*>(v_cache), d->n_tokens, d->kv_dim, d->base_pos,
+                           d->window);
+    LMX_CHECK_LAUNCH();
+    return LMX_OK;
+}
+
+size_t lmx_attn_workspace_bytes(const lmx_attn_params* p) {
+    if (check_attn_params(p) != LMX_OK) return 0;
+    // The split-K path is the only one with a workspace; f32 q is the case
+    // that decides between the paths most conservatively.
+    if (!use_split_k(p, LMX_F32) && !use_split_k(p, LMX_F16)) return 0;
+    return decode_workspace_bytes(p);
+}
+
+lmx_status lmx_attn_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt,
+                        const void* k_cache, const void* v_cache, lmx_dtype kv_dt,
+                        const void* k_cur, const void* v_cur, float* out, void* ws,
+                        size_t ws_bytes, lmx_stream stream) {
+    lmx_status s = check_attn_params(p);
+    if (s != LMX_OK) return s;
+    if (q_dt != LMX_F32 && q_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if (kv_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if (!q || !k_cache || !v_cache || !out) return LMX_E_NULL;
+    if ((k_cur == nullptr) != (v_cur == nullptr)) return LMX_E_NULL;
+    if (p->window && p->n_tokens > 1 && (uint64_t)p->base_pos + p->n_tokens > p->window && !k_cur)
+        return LMX_E_RING_HAZARD;
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 16))
+        return LMX_E_ALIGN;
+    if (k_cur && (!aligned(k_cur, 16) || !aligned(v_cur, 16))) return LMX_E_ALIGN;
+    if (use_split_k(p, q_dt))
+        return decode_fwd(p, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
+                          (hipStream_t)stream);
+    return prefill_fwd(p, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, (hipStream_t)stream);
+}
+
+size_t lmx_attn_decode_batched_workspace_bytes(const lmx_attn_params* p, int32_t n_seq,
+                                               int32_t max_ctx) {
+    if (!p || n_seq < 1 || max_ctx < 1) return 0;
+    if (!p->n_kv_heads || !p->n_heads || p->n_heads % p->n_kv_heads) return 0;
+    return decode_batched_workspace_bytes(p, n_seq, max_ctx);
+}
+
+lmx_status lmx_attn_decode_batched(const lmx_attn_params* p, int32_t n_seq, int32_t max_ctx,
+                                   const int32_t* ctx_lens, const void* const* k_ptrs,
+                                   const void* const* v_ptrs, const void* q, lmx_dtype q_dt,
+                                   lmx_dtype kv_dt, float* out, void* ws, size_t ws_bytes,
+                                   lmx_stream stream) {
+    if (!p) return LMX_E_NULL;
+    if (p->n_tokens != 1 || n_seq < 1 || max_ctx < 1) return LMX_E_SHAPE;
+    lmx_attn_params pp = *p;
+    pp.base_pos = 0;
+    lmx_status s = check_attn_params(&pp);
+    if (s != LMX_OK) return s;
+    if (p->bidi) return LMX_E_SHAPE;
+    if (p->window == 0 && (uint32_t)max_ctx > p->n_slots) return LMX_E_CONTEXT;
+    if (q_dt != LMX_F32 && q_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if (kv_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if (!ctx_lens || !k_ptrs || !v_ptrs || !q || !out) return LMX_E_NULL;
+    if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_ptrs, 8) || !aligned(v_ptrs, 8) ||
+        !aligned(ctx_lens, 4))
+        return LMX_E_ALIGN;
+    return decode_batched(p, n_seq, max_ctx, ctx_lens, k_ptrs, v_ptrs, q, q_dt, out, ws, ws_bytes,
+                          (hipStream_t)stream);
+}
+
+static lmx_status check_dop(const lmx_dop* op) {
+    if (!op) return LMX_E_NULL;
+    if (!op->n_tok || !op->n_vh || !op->n_kh || !op->s_dim) return LMX_E_SHAPE;
+    if (op->s_dim != 128 && op->s_dim != 64) return LMX_E_UNSUPPORTED;
+    if (op->key_dim != op->n_kh * op->s_dim || op->d_inner != op->n_vh * op->s_dim) return LMX_E_SHAPE;
+    if (op->conv_dim < 2 * op->key_dim + op->d_inner || op->conv_dim % 4) return LMX_E_SHAPE;
+    if (!std::isfinite(op->scale)) return LMX_E_SHAPE;
+    return LMX_OK;
+}
+
+lmx_status lmx_deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
+                              const float* alpha, const float* beta, const float* conv,
+                              float* state, float* out, lmx_stream stream) {
+    lmx_status s = check_dop(op);
+    if (s != LMX_OK) return s;
+    if (!ssm_a || !dt_bias || !alpha || !beta || !conv || !state || !out) return LMX_E_NULL;
+    if (!aligned(conv, 16) || !aligned(state, 16) || !aligned(out, 16)) return LMX_E_ALIGN;
+    return deltanet_recur(op, ssm_a, dt_bias, alpha, beta, conv, state, out, (hipStream_t)stream);
+}
+
+size_t lmx_deltanet_chunked_workspace_bytes(const lmx_dop* op, int32_t chunk) {
+    if (check_dop(op) != LMX_OK) return 0;
+    if (chunk != 16 && chunk != 32 && chunk != 64) return 0;
+    return deltanet_chunked_ws(op, chunk);
+}
+
+lmx_status lmx_deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
+                                const float* alpha, const float* beta, const float* conv,
+                                float* state, float* out, int32_t chunk, void* ws,
+                                size_t ws_bytes, lmx_stream stream) {
+    lmx_status s = check_dop(op);
+    if (s != LMX_OK) return s;
+    if (chunk != 16 && chunk != 32 && chunk != 64) return LMX_E_SHAPE;
+    if (!ssm_a || !dt_bias || !alpha || !beta || !conv || !state || !out) return LMX_E_NULL;
+    if (!aligned(conv, 16) || !aligned(state, 16) || !aligned(out, 16)) return LMX_E_ALIGN;
+    const size_t need = deltanet_chunked_ws(op, chunk);
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return LMX_E_WORKSPACE;
+        if (!aligned(ws, 256)) return LMX_E_ALIGN;
+    }
+    return deltanet_chunked(op, ssm_a, dt_bias, alpha, beta, conv, state, out, chunk, ws, ws_bytes,
+                            (hipStream_t)stream);
+}
+
+}  // extern "C"

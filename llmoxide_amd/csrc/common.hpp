@@ -1,0 +1,108 @@
+// Shared device helpers for the gfx950 kernels of libllmoxide_amd.
+//
+// Wave64 only: every cross-lane helper here assumes 64-lane wavefronts and
+// uses DPP row operations (16-lane rows), which is what CDNA4 executes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lmx/attn.h"
+
+namespace lmx {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// v_exp_f32: 2^x, exact 0 for -inf.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x141>(x);  // row_half_mirror: pairs the two quads of each half-row
+    x += dpp<0x140>(x);  // row_mirror: pairs the two half-rows
+    return x;
+}
+
+__device__ __forceinline__ float shfl_xor(float x, int m) { return __shfl_xor(x, m, 64); }
+
+// Load N consecutive f16 values (N a multiple of 4) as floats.
+template <int N>
+__device__ __forceinline__ void load_f16_as_f32(const f16* __restrict__ p, float (&out)[N]) {
+    static_assert(N % 4 == 0, "vector width");
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            f16x8 v = *reinterpret_cast<const f16x8*>(p + 8 * i);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out[8 * i + j] = (float)v[j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            f16x4 v = *reinterpret_cast<const f16x4*>(p + 4 * i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out[4 * i + j] = (float)v[j];
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&out)[N]) {
+    static_assert(N % 4 == 0, "vector width");
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[4 * i + j] = v[j];
+    }
+}
+
+// Raw f16 lanes held in registers (no conversion), N a multiple of 4.
+template <int N>
+struct RawF16 {
+    static_assert(N % 4 == 0, "vector width");
+    f16x4 v[N / 4];
+};
+
+template <int N>
+__device__ __forceinline__ void load_raw(const f16* __restrict__ p, RawF16<N>& r) {
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            f16x8 x = *reinterpret_cast<const f16x8*>(p + 8 * i);
+            r.v[2 * i] = f16x4{x[0], x[1], x[2], x[3]};
+            r.v[2 * i + 1] = f16x4{x[4], x[5], x[6], x[7]};
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) r.v[i] = *reinterpret_cast<const f16x4*>(p + 4 * i);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float raw_at(const RawF16<N>& r, int i) {
+    return (float)r.v[i / 4][i % 4];
+}
+
+}  // namespace lmx
+
+// Host-side helpers shared by the entry points.
+#define LMX_CHECK_LAUNCH()                                  \
+    do {                                                    \
+        if (hipGetLastError() != hipSuccess) return LMX_E_LAUNCH; \
+    } while (0)

@@ -1,0 +1,219 @@
+"""CPU oracle for llmoxide's attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg import this package, and only as the checker (or the timed CPU baseline),
+never as the thing measured or shipped.  The product path (``llmoxide_amd``)
+never imports it and fails loudly when its HIP library is missing.
+
+Two layers:
+
+* ``liblmx_oracle.so`` (``lmx_oracle.c``): the C restatement of the reference's
+  scalar loops, same loop and summation order in f32.  Reference lines are
+  cited per function in the C file.
+* ``textbook``: independent float64 NumPy formulations (matrix form, masks as
+  boolean matrices) used only to pin the C restatement.  They share no code
+  with it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liblmx_oracle.so")
+
+
+def build(force: bool = False) -> str:
+    """Compile liblmx_oracle.so with the committed Makefile."""
+    if force or not os.path.exists(_LIB_PATH) or (
+        os.path.getmtime(_LIB_PATH) < os.path.getmtime(os.path.join(_HERE, "lmx_oracle.c"))
+    ):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"], check=True)
+    return _LIB_PATH
+
+
+class OrcAttn(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", ctypes.c_uint32),
+        ("n_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("kv_dim", ctypes.c_uint32),
+        ("base_pos", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("bidi", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class OrcDop(ctypes.Structure):
+    _fields_ = [
+        ("n_tok", ctypes.c_uint32),
+        ("conv_dim", ctypes.c_uint32),
+        ("key_dim", ctypes.c_uint32),
+        ("d_inner", ctypes.c_uint32),
+        ("s_dim", ctypes.c_uint32),
+        ("n_vh", ctypes.c_uint32),
+        ("n_kh", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.POINTER
+        f32p, u16p = P(ctypes.c_float), P(ctypes.c_uint16)
+        L.orc_fill_uniform.argtypes = [ctypes.c_uint64, f32p, ctypes.c_size_t]
+        L.orc_fill_normal.argtypes = [ctypes.c_uint64, f32p, ctypes.c_size_t]
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_to_f16.argtypes = [f32p, u16p, ctypes.c_size_t]
+        L.orc_from_f16.argtypes = [u16p, f32p, ctypes.c_size_t]
+        L.orc_slot.argtypes = [ctypes.c_int64, ctypes.c_int64]
+        L.orc_slot.restype = ctypes.c_int64
+        L.orc_visible.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int, P(ctypes.c_int64), P(ctypes.c_int64)]
+        L.orc_softmax.argtypes = [f32p, ctypes.c_size_t]
+        L.orc_write_cache.argtypes = [ctypes.c_int64] * 4 + [f32p, u16p]
+        L.orc_attention.argtypes = [P(OrcAttn), f32p, f32p, f32p, f32p, ctypes.c_int, ctypes.c_int]
+        L.orc_attention.restype = ctypes.c_int
+        L.orc_delta_recur.argtypes = [P(OrcDop)] + [f32p] * 7
+        L.orc_l2_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
+        L.orc_rms_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
+        _lib = L
+    return _lib
+
+
+def _f32p(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _u16p(a: np.ndarray):
+    assert a.dtype == np.uint16 and a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+# ------------------------------------------------------------------ inputs --
+def uniform(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_uniform(seed, _f32p(out), n)
+    return out
+
+
+def normal(seed: int, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(seed, _f32p(out), n)
+    return out.reshape(shape)
+
+
+def to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_to_f16(_f32p(x), _u16p(out), x.size)
+    return out
+
+
+def from_f16_bits(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_from_f16(_u16p(h), _f32p(out), h.size)
+    return out
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    """x rounded to the nearest f16 value, returned as f32."""
+    return from_f16_bits(to_f16_bits(x))
+
+
+def rms_norm_rows(x: np.ndarray, dim: int, eps: float = 1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).copy()
+    lib().orc_rms_norm_rows(_f32p(x), x.size // dim, dim, eps)
+    return x
+
+
+def l2_norm_rows(x: np.ndarray, dim: int, eps: float = 1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).copy()
+    lib().orc_l2_norm_rows(_f32p(x), x.size // dim, dim, eps)
+    return x
+
+
+# ------------------------------------------------------------- bookkeeping --
+def slot(pos: int, window: int) -> int:
+    return lib().orc_slot(pos, window)
+
+
+def visible(pos: int, window: int, base_pos: int, n_tokens: int, bidi: bool):
+    lo, hi = ctypes.c_int64(), ctypes.c_int64()
+    lib().orc_visible(pos, window, base_pos, n_tokens, int(bidi), ctypes.byref(lo), ctypes.byref(hi))
+    return lo.value, hi.value
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).copy()
+    lib().orc_softmax(_f32p(x), x.size)
+    return x
+
+
+def write_cache(src: np.ndarray, cache_bits: np.ndarray, base_pos: int, window: int) -> np.ndarray:
+    """Store f32 rows src[t, kv_dim] into an f16 cache (bits), in place."""
+    src = np.ascontiguousarray(src, np.float32)
+    t, kv_dim = src.shape
+    assert cache_bits.dtype == np.uint16 and cache_bits.shape[1] == kv_dim
+    lib().orc_write_cache(t, kv_dim, base_pos, window, _f32p(src), _u16p(cache_bits))
+    return cache_bits
+
+
+# --------------------------------------------------------------- attention --
+def attention(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, window=0,
+              bidi=False, scale=None, linear=True, n_threads=1, kv_dim=None):
+    """Reference attention (cpu.rs:342-387; qwen35/cpu.rs:324-365).
+
+    q: [t, H*hd] f32.  k, v: f32 rows, by absolute position when ``linear``
+    (shape [>= base_pos+t, kv_dim]), else by ring slot (the reference's cache
+    after its store).  Returns out [t, H*hd] f32.
+    """
+    q = np.ascontiguousarray(q, np.float32).reshape(-1, n_heads * head_dim)
+    t = q.shape[0]
+    kv_dim = kv_dim or n_kv_heads * head_dim
+    k = np.ascontiguousarray(k, np.float32).reshape(-1, kv_dim)
+    v = np.ascontiguousarray(v, np.float32).reshape(-1, kv_dim)
+    p = OrcAttn(t, n_heads, n_kv_heads, head_dim, kv_dim, base_pos, window, int(bidi),
+                float(np.float32(1.0) / np.sqrt(np.float32(head_dim))) if scale is None else float(scale))
+    out = np.zeros((t, n_heads * head_dim), np.float32)
+    rc = lib().orc_attention(ctypes.byref(p), _f32p(q), _f32p(k), _f32p(v), _f32p(out),
+                             int(linear), int(n_threads))
+    if rc != 0:
+        raise ValueError("orc_attention: invalid shape")
+    return out
+
+
+def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=None):
+    """Gated delta rule (qwen35/cpu.rs:218-245).  Returns (out, S_new)."""
+    conv = np.ascontiguousarray(conv, np.float32)
+    n_tok, conv_dim = conv.shape
+    key_dim, d_inner = n_kh * s_dim, n_vh * s_dim
+    assert conv_dim == 2 * key_dim + d_inner
+    alpha = np.ascontiguousarray(alpha, np.float32).reshape(n_tok, n_vh)
+    beta = np.ascontiguousarray(beta, np.float32).reshape(n_tok, n_vh)
+    ssm_a = np.full(n_vh, -1.0, np.float32) if ssm_a is None else np.ascontiguousarray(ssm_a, np.float32)
+    dt_bias = np.zeros(n_vh, np.float32) if dt_bias is None else np.ascontiguousarray(dt_bias, np.float32)
+    S = np.ascontiguousarray(S, np.float32).copy()
+    out = np.zeros((n_tok, d_inner), np.float32)
+    op = OrcDop(n_tok, conv_dim, key_dim, d_inner, s_dim, n_vh, n_kh,
+                np.float32(1.0) / np.sqrt(np.float32(s_dim)))
+    lib().orc_delta_recur(ctypes.byref(op), _f32p(ssm_a), _f32p(dt_bias), _f32p(alpha),
+                          _f32p(beta), _f32p(conv), _f32p(S), _f32p(out))
+    return out, S

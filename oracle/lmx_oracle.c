@@ -1,0 +1,362 @@
+/*
+ * lmx_oracle.c -- CPU restatement of llmoxide's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (llmoxide_amd/, include/)
+ * links, loads or calls this file.  It is the parity checker for the HIP
+ * kernels and the CPU baseline that bench.py reports next to the GPU figure.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+ *
+ * Every function follows a named piece of the reference (paths relative to the
+ * llmoxide source tree) and keeps its loop and summation order: plain f32,
+ * products rounded before the add (built with -ffp-contract=off, no fast-math),
+ * libm expf / logf as Rust's f32::exp / ln call them on Linux.
+ *
+ * Parity pins (checked in tests/test_oracle_*.py):
+ *   orc_rng_*            crates/model/src/sample.rs:73-92, pinned by
+ *                        a hand-computed xorshift64* trace.
+ *   orc_f32_to_f16 /     IEEE binary16 round-to-nearest-even, pinned against
+ *   orc_f16_to_f32       numpy's float16 over all 65536 codes and 1e6 floats.
+ *   orc_slot/visible     crates/model/src/cache.rs:21-38 + attn.wgsl:52-80,
+ *                        pinned by the ported known-answer tests
+ *                        (cache.rs:169-204) and brute-force enumeration.
+ *   orc_softmax          crates/model/src/ops.rs:119-135, pinned by the ported
+ *                        KATs (ops.rs:259-273) and float64 closed form.
+ *   orc_write_cache      ops.wgsl:323-346 / cache.rs:58-62, pinned by a
+ *                        brute-force last-writer-wins simulation.
+ *   orc_attention        crates/model/src/cpu.rs:342-387 and
+ *                        crates/model/src/qwen35/cpu.rs:324-365, pinned by an
+ *                        independent float64 matrix-form implementation, by
+ *                        torch scaled_dot_product_attention with an explicit
+ *                        mask, and by invariants (one visible key -> out = v,
+ *                        GQA == head-expanded MHA, constant V -> out = V).
+ *   orc_delta_recur      crates/model/src/qwen35/cpu.rs:218-245 (and the GPU
+ *                        form deltanet.wgsl:193-239), pinned by a float64
+ *                        matrix restatement and by invariants (exact write at
+ *                        g=1,beta=1 with unit k; beta=0 pure decay; linearity
+ *                        in v; orthonormal keys write independently).
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ rng -- */
+/* xorshift64*, crates/model/src/sample.rs:73-92. */
+typedef struct { uint64_t s; } orc_rng;
+
+void orc_rng_init(orc_rng *r, uint64_t seed) {
+    r->s = (seed * 0x9E3779B97F4A7C15ull) | 1ull;
+}
+
+float orc_rng_next_f32(orc_rng *r) {
+    uint64_t x = r->s;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    r->s = x;
+    return (float)((x * 0x2545F4914F6CDD1Dull) >> 40) / (float)(1u << 24);
+}
+
+/* n uniforms in [0,1) from one seed. */
+void orc_fill_uniform(uint64_t seed, float *out, size_t n) {
+    orc_rng r;
+    orc_rng_init(&r, seed);
+    for (size_t i = 0; i < n; ++i) out[i] = orc_rng_next_f32(&r);
+}
+
+/* n N(0,1) draws: Box-Muller, one normal per pair of uniforms, u1 -> 1-u1 so
+ * the log argument is in (0,1].  Computed in double, rounded to f32 once. */
+void orc_fill_normal(uint64_t seed, float *out, size_t n) {
+    orc_rng r;
+    orc_rng_init(&r, seed);
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; ++i) {
+        double u1 = 1.0 - (double)orc_rng_next_f32(&r);
+        double u2 = (double)orc_rng_next_f32(&r);
+        out[i] = (float)(sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+    }
+}
+
+/* ------------------------------------------------------------------ f16 -- */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ex = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (ex == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    int e = (int)ex - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        int shift = 14 - e;
+        uint32_t h = man >> shift;
+        uint32_t rem = man & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)h;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t ex = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t man = (uint32_t)h & 0x3ffu;
+    uint32_t x;
+    if (ex == 0) {
+        if (man == 0) {
+            x = sign;
+        } else {
+            int e = -1;
+            do { man <<= 1; ++e; } while (!(man & 0x400u));
+            man &= 0x3ffu;
+            x = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (ex == 31) {
+        x = sign | 0x7f800000u | (man << 13);
+    } else {
+        x = sign | ((ex - 15 + 127) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void orc_to_f16(const float *in, uint16_t *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16(in[i]);
+}
+
+void orc_from_f16(const uint16_t *in, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(in[i]);
+}
+
+/* --------------------------------------------------------- bookkeeping -- */
+/* cache.rs:21-28 (LayerCache::slot), attn.wgsl:68-71 (cache_slot). */
+int64_t orc_slot(int64_t pos, int64_t window) {
+    return window ? pos % window : pos;
+}
+
+/* Visible key positions [*lo, *hi] of the query at `pos`.
+ * Causal: cache.rs:30-38 (visible), attn.wgsl:52-56 (first_visible).
+ * Bidirectional end: cpu.rs:351-360, attn.wgsl:58-66 (last_visible). */
+void orc_visible(int64_t pos, int64_t window, int64_t base_pos, int64_t n_tokens,
+                 int bidi, int64_t *lo, int64_t *hi) {
+    *lo = window ? (pos + 1 <= window ? 0 : pos + 1 - window) : 0;
+    if (!bidi) {
+        *hi = pos;
+    } else {
+        int64_t end = base_pos + n_tokens - 1;
+        if (!window) {
+            *hi = end;
+        } else {
+            int64_t h = pos + window - 1;
+            *hi = end < h ? end : h;
+        }
+    }
+}
+
+/* ------------------------------------------------------------- softmax -- */
+/* ops.rs:119-135: max-subtracted, an all -inf row becomes zeros. */
+void orc_softmax(float *x, size_t n) {
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
+    if (!isfinite(mx)) {
+        for (size_t i = 0; i < n; ++i) x[i] = 0.0f;
+        return;
+    }
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        x[i] = expf(x[i] - mx);
+        sum += x[i];
+    }
+    float inv = 1.0f / sum;
+    for (size_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+/* --------------------------------------------------------- write_cache -- */
+/* ops.wgsl:323-346 and cache.rs:58-62: row i of the batch lands in slot
+ * slot(base_pos + i); rows are stored in order, so within one call a later
+ * position that maps to the same ring slot wins.  The cache holds f16. */
+void orc_write_cache(int64_t n_tokens, int64_t kv_dim, int64_t base_pos,
+                     int64_t window, const float *src, uint16_t *cache) {
+    for (int64_t i = 0; i < n_tokens; ++i) {
+        int64_t s = orc_slot(base_pos + i, window);
+        for (int64_t d = 0; d < kv_dim; ++d)
+            cache[s * kv_dim + d] = orc_f32_to_f16(src[i * kv_dim + d]);
+    }
+}
+
+/* ----------------------------------------------------------- attention -- */
+typedef struct {
+    uint32_t n_tokens, n_heads, n_kv_heads, head_dim, kv_dim;
+    uint32_t base_pos, window, bidi;
+    float scale;
+} orc_attn;
+
+typedef struct {
+    const orc_attn *p;
+    const float *q, *k, *v;
+    float *out;
+    int linear;           /* 1: k/v indexed by position; 0: by ring slot */
+    int64_t begin, end;   /* (token, head) work items [begin, end) */
+} orc_attn_job;
+
+static void *orc_attn_run(void *arg) {
+    const orc_attn_job *j = (const orc_attn_job *)arg;
+    const orc_attn *p = j->p;
+    const int64_t hd = p->head_dim, kvd = p->kv_dim, H = p->n_heads;
+    const int64_t group = p->n_heads / p->n_kv_heads;
+    const int64_t win = p->window;
+    int64_t cap = (int64_t)p->base_pos + p->n_tokens + 1;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)cap);
+    for (int64_t item = j->begin; item < j->end; ++item) {
+        const int64_t i = item / H, hq = item % H;
+        const int64_t pos = (int64_t)p->base_pos + i;
+        int64_t lo, hi;
+        orc_visible(pos, win, p->base_pos, p->n_tokens, (int)p->bidi, &lo, &hi);
+        const int64_t n_vis = hi - lo + 1;
+        const int64_t kv_head = hq / group;
+        const float *qh = j->q + (i * H + hq) * hd;
+        /* cpu.rs:362-368: scores over the window, sequential f32 sum. */
+        for (int64_t s = 0; s < n_vis; ++s) {
+            const int64_t pp = lo + s;
+            const int64_t row = j->linear ? pp : orc_slot(pp, win);
+            const float *kh = j->k + row * kvd + kv_head * hd;
+            float acc = 0.0f;
+            for (int64_t d = 0; d < hd; ++d) acc += qh[d] * kh[d];
+            scores[s] = acc * p->scale;
+        }
+        orc_softmax(scores, (size_t)n_vis);
+        /* cpu.rs:371-385: weighted sum, zero weights skipped. */
+        float *out = j->out + (i * H + hq) * hd;
+        for (int64_t d = 0; d < hd; ++d) out[d] = 0.0f;
+        for (int64_t s = 0; s < n_vis; ++s) {
+            const float w = scores[s];
+            if (w == 0.0f) continue;
+            const int64_t pp = lo + s;
+            const int64_t row = j->linear ? pp : orc_slot(pp, win);
+            const float *vh = j->v + row * kvd + kv_head * hd;
+            for (int64_t d = 0; d < hd; ++d) out[d] += w * vh[d];
+        }
+    }
+    free(scores);
+    return NULL;
+}
+
+/* Attention over K/V rows.  linear = 0 reads the reference's cache layout:
+ * rows are ring slots, the batch has already been stored (cpu.rs:332-339 then
+ * 343-387).  linear = 1 reads rows by absolute position (the documented window
+ * semantics over keys that hold every visible position).  n_threads > 1 splits
+ * the (token, head) items over pthreads; each item's arithmetic is unchanged.
+ * Returns 0, or -1 on an invalid shape. */
+int orc_attention(const orc_attn *p, const float *q, const float *k,
+                  const float *v, float *out, int linear, int n_threads) {
+    if (!p->n_tokens || !p->n_heads || !p->n_kv_heads || !p->head_dim) return -1;
+    if (p->n_heads % p->n_kv_heads) return -1;
+    if (p->kv_dim < p->n_kv_heads * p->head_dim) return -1;
+    const int64_t items = (int64_t)p->n_tokens * p->n_heads;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > items) n_threads = (int)items;
+    orc_attn_job jobs[256];
+    pthread_t th[256];
+    if (n_threads > 256) n_threads = 256;
+    for (int t = 0; t < n_threads; ++t) {
+        jobs[t].p = p;
+        jobs[t].q = q;
+        jobs[t].k = k;
+        jobs[t].v = v;
+        jobs[t].out = out;
+        jobs[t].linear = linear;
+        jobs[t].begin = items * t / n_threads;
+        jobs[t].end = items * (t + 1) / n_threads;
+    }
+    if (n_threads == 1) {
+        orc_attn_run(&jobs[0]);
+        return 0;
+    }
+    for (int t = 0; t < n_threads; ++t) pthread_create(&th[t], NULL, orc_attn_run, &jobs[t]);
+    for (int t = 0; t < n_threads; ++t) pthread_join(th[t], NULL);
+    return 0;
+}
+
+/* --------------------------------------------------------- delta rule -- */
+typedef struct {
+    uint32_t n_tok, conv_dim, key_dim, d_inner, s_dim, n_vh, n_kh;
+    float scale; /* 1/sqrt(s_dim), qwen35.rs:923 / qwen35/cpu.rs:166 */
+} orc_dop;
+
+/* ops.rs:187-193 */
+static float orc_softplus(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+/* ops.rs:181-183 */
+static float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* qwen35/cpu.rs:218-245: the gated delta rule over n_tok tokens.
+ *   conv   [n_tok, conv_dim]  channels q(key_dim) | k(key_dim) | v(d_inner),
+ *                             q and k already L2-normalized per head
+ *   alpha  [n_tok, n_vh]      raw decay projection
+ *   beta   [n_tok, n_vh]      raw mixing projection
+ *   ssm_a, dt_bias [n_vh]
+ *   S      [n_vh, s_dim (value row j), s_dim (key col)]  updated in place
+ *   out    [n_tok, d_inner]
+ * The v-head -> k-head map tiles: hk = hv % n_kh (cpu.rs:220). */
+void orc_delta_recur(const orc_dop *op, const float *ssm_a, const float *dt_bias,
+                     const float *alpha, const float *beta, const float *conv,
+                     float *S, float *out) {
+    const int64_t sd = op->s_dim;
+    for (int64_t i = 0; i < op->n_tok; ++i) {
+        const float *row_c = conv + i * op->conv_dim;
+        const float *qn = row_c;
+        const float *kn = row_c + op->key_dim;
+        const float *vals = row_c + 2 * op->key_dim;
+        float *o = out + i * op->d_inner;
+        for (int64_t hv = 0; hv < op->n_vh; ++hv) {
+            const int64_t hk = (hv % op->n_kh) * sd;
+            const float *qh = qn + hk, *kh = kn + hk, *vh = vals + hv * sd;
+            const float g = expf(ssm_a[hv] * orc_softplus(alpha[i * op->n_vh + hv] + dt_bias[hv]));
+            const float bmix = orc_sigmoid(beta[i * op->n_vh + hv]);
+            float *sh = S + hv * sd * sd;
+            for (int64_t x = 0; x < sd * sd; ++x) sh[x] *= g;
+            float *oh = o + hv * sd;
+            for (int64_t jr = 0; jr < sd; ++jr) {
+                float *r = sh + jr * sd;
+                float pred = 0.0f;
+                for (int64_t d = 0; d < sd; ++d) pred += r[d] * kh[d];
+                const float delta = (vh[jr] - pred) * bmix;
+                for (int64_t d = 0; d < sd; ++d) r[d] += delta * kh[d];
+                float acc = 0.0f;
+                for (int64_t d = 0; d < sd; ++d) acc += r[d] * qh[d];
+                oh[jr] = acc * op->scale;
+            }
+        }
+    }
+}
+
+/* ops.rs:197-203: x / max(||x||, eps), per head of `dim` elements. */
+void orc_l2_norm_rows(float *x, int64_t rows, int64_t dim, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float *v = x + r * dim;
+        float acc = 0.0f;
+        for (int64_t d = 0; d < dim; ++d) acc += v[d] * v[d];
+        float nrm = sqrtf(acc);
+        float sc = 1.0f / (nrm > eps ? nrm : eps);
+        for (int64_t d = 0; d < dim; ++d) v[d] *= sc;
+    }
+}
+
+/* ops.rs:40-47: x / sqrt(mean(x^2) + eps), per head of `dim` elements. */
+void orc_rms_norm_rows(float *x, int64_t rows, int64_t dim, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float *v = x + r * dim;
+        float acc = 0.0f;
+        for (int64_t d = 0; d < dim; ++d) acc += v[d] * v[d];
+        float mean_sq = acc / (float)dim;
+        float sc = 1.0f / sqrtf(mean_sq + eps);
+        for (int64_t d = 0; d < dim; ++d) v[d] *= sc;
+    }
+}

@@ -1,0 +1,130 @@
+"""Independent float64 formulations used only to pin the C oracle.
+
+TEST INFRASTRUCTURE ONLY.  These are written from the mathematics, not from
+the reference's loops: attention is ``softmax(scale * Q K^T + mask) V`` with
+the mask built as a boolean matrix; the delta rule is the matrix recurrence
+``S_t = g_t S_{t-1} (I - b_t k_t k_t^T) + b_t v_t k_t^T``; the chunked delta rule
+is the WY/UT form.  None of them shares code with lmx_oracle.c.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def mask_matrix(t: int, n_keys: int, base_pos: int, window: int, bidi: bool) -> np.ndarray:
+    """Boolean [t, n_keys]: query i (at base_pos+i) may see key position p.
+
+    Causal window: p in [pos-w+1, pos] (or [0, pos] when w == 0).  With bidi the
+    upper edge becomes the batch end, still within w-1 ahead of the query.
+    """
+    pos = base_pos + np.arange(t)[:, None]
+    p = np.arange(n_keys)[None, :]
+    ok = p <= pos
+    if bidi:
+        end = base_pos + t - 1
+        ok = np.broadcast_to(p <= end, (t, n_keys)).copy()
+        if window:
+            ok &= p <= pos + window - 1
+    if window:
+        ok &= p >= pos - window + 1
+    return ok
+
+
+def attention(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, window=0,
+              bidi=False, scale=None):
+    """float64 GQA attention over keys indexed by absolute position."""
+    q = np.asarray(q, np.float64).reshape(-1, n_heads, head_dim)
+    t = q.shape[0]
+    k = np.asarray(k, np.float64).reshape(-1, n_kv_heads, head_dim)
+    v = np.asarray(v, np.float64).reshape(-1, n_kv_heads, head_dim)
+    n_keys = k.shape[0]
+    scale = 1.0 / np.sqrt(head_dim) if scale is None else float(scale)
+    g = n_heads // n_kv_heads
+    kh = np.repeat(k, g, axis=1)  # [n_keys, H, hd], head h reads kv head h // g
+    vh = np.repeat(v, g, axis=1)
+    s = np.einsum("thd,phd->htp", q, kh) * scale
+    m = mask_matrix(t, n_keys, base_pos, window, bidi)[None]
+    s = np.where(m, s, -np.inf)
+    mx = s.max(axis=-1, keepdims=True)
+    e = np.where(m, np.exp(s - mx), 0.0)
+    p = e / e.sum(axis=-1, keepdims=True)
+    o = np.einsum("htp,phd->thd", p, vh)
+    return o.reshape(t, n_heads * head_dim)
+
+
+def softplus(x):
+    x = np.asarray(x, np.float64)
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def gates(alpha, beta, ssm_a, dt_bias):
+    """Per (token, v-head) decay g = exp(a * softplus(alpha + dt)), mix sigmoid(beta)."""
+    g = np.exp(np.asarray(ssm_a, np.float64)[None] * softplus(np.asarray(alpha, np.float64) + np.asarray(dt_bias, np.float64)[None]))
+    b = 1.0 / (1.0 + np.exp(-np.asarray(beta, np.float64)))
+    return g, b
+
+
+def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=None):
+    """float64 matrix form: S <- g S (I - b k k^T) + b v k^T ; o = S q / sqrt(d)."""
+    conv = np.asarray(conv, np.float64)
+    n_tok = conv.shape[0]
+    key_dim = n_kh * s_dim
+    ssm_a = -np.ones(n_vh) if ssm_a is None else ssm_a
+    dt_bias = np.zeros(n_vh) if dt_bias is None else dt_bias
+    g, b = gates(np.asarray(alpha).reshape(n_tok, n_vh), np.asarray(beta).reshape(n_tok, n_vh), ssm_a, dt_bias)
+    S = np.asarray(S, np.float64).reshape(n_vh, s_dim, s_dim).copy()
+    out = np.zeros((n_tok, n_vh * s_dim))
+    eye = np.eye(s_dim)
+    for t in range(n_tok):
+        for hv in range(n_vh):
+            hk = hv % n_kh
+            q = conv[t, hk * s_dim:(hk + 1) * s_dim]
+            k = conv[t, key_dim + hk * s_dim:key_dim + (hk + 1) * s_dim]
+            v = conv[t, 2 * key_dim + hv * s_dim:2 * key_dim + (hv + 1) * s_dim]
+            S[hv] = g[t, hv] * S[hv] @ (eye - b[t, hv] * np.outer(k, k)) + b[t, hv] * np.outer(v, k)
+            out[t, hv * s_dim:(hv + 1) * s_dim] = S[hv] @ q / np.sqrt(s_dim)
+    return out, S.reshape(-1)
+
+
+def delta_chunked(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, chunk, ssm_a=None, dt_bias=None):
+    """float64 chunked (WY/UT) form of the same recurrence.
+
+    Per chunk of C tokens with cumulative in-chunk decay gamma_t = prod g:
+      A[t,i]  = b_t (gamma_t/gamma_i) k_t.k_i            (i < t)
+      U       = (I+A)^-1 (diag(b) V - diag(b gamma) K S0^T)
+      O       = diag(gamma) Q S0^T + (tril(QK^T) * gamma_t/gamma_i) U
+      S_C     = gamma_C S0 + U^T diag(gamma_C/gamma) K
+    """
+    conv = np.asarray(conv, np.float64)
+    n_tok = conv.shape[0]
+    key_dim = n_kh * s_dim
+    ssm_a = -np.ones(n_vh) if ssm_a is None else ssm_a
+    dt_bias = np.zeros(n_vh) if dt_bias is None else dt_bias
+    g, b = gates(np.asarray(alpha).reshape(n_tok, n_vh), np.asarray(beta).reshape(n_tok, n_vh), ssm_a, dt_bias)
+    S = np.asarray(S, np.float64).reshape(n_vh, s_dim, s_dim).copy()
+    out = np.zeros((n_tok, n_vh * s_dim))
+    for hv in range(n_vh):
+        hk = hv % n_kh
+        Q = conv[:, hk * s_dim:(hk + 1) * s_dim]
+        K = conv[:, key_dim + hk * s_dim:key_dim + (hk + 1) * s_dim]
+        V = conv[:, 2 * key_dim + hv * s_dim:2 * key_dim + (hv + 1) * s_dim]
+        S0 = S[hv]
+        for c0 in range(0, n_tok, chunk):
+            c1 = min(n_tok, c0 + chunk)
+            Qc, Kc, Vc = Q[c0:c1], K[c0:c1], V[c0:c1]
+            lg = np.cumsum(np.log(g[c0:c1, hv]))
+            bc = b[c0:c1, hv]
+            n = c1 - c0
+            lower = np.tril(np.ones((n, n), bool))
+            # gamma_t / gamma_i on and below the diagonal, 0 above (never exp'd)
+            ratio = np.where(lower, np.exp(np.where(lower, lg[:, None] - lg[None, :], 0.0)), 0.0)
+            A = np.tril(bc[:, None] * ratio * (Kc @ Kc.T), -1)
+            gam = np.exp(lg)
+            rhs = bc[:, None] * Vc - (bc * gam)[:, None] * (Kc @ S0.T)
+            U = np.linalg.solve(np.eye(n) + A, rhs)
+            P = np.tril(Qc @ Kc.T) * ratio
+            O = gam[:, None] * (Qc @ S0.T) + P @ U
+            out[c0:c1, hv * s_dim:(hv + 1) * s_dim] = O / np.sqrt(s_dim)
+            S0 = gam[-1] * S0 + (U * np.exp(lg[-1] - lg)[:, None]).T @ Kc
+        S[hv] = S0
+    return out, S.reshape(-1)

@@ -1,0 +1,144 @@
+"""The C-ABI library loads, exports every symbol include/lmx/attn.h declares,
+and rejects bad arguments on the host (no GPU needed: every call here returns
+before anything is enqueued)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import llmoxide_amd as lmx
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lmx", "attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lmx_\w+)\s*\(", text)))
+
+
+def test_header_compiles_as_c_and_cxx(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "lmx/attn.h"\nint main(void){return lmx_version()==0;}\n')
+    for cc, extra in (("gcc", ["-std=c99"]), ("g++", ["-x", "c++", "-std=c++17"])):
+        r = subprocess.run([cc, *extra, "-fsyntax-only", "-Wall", "-Werror", "-I",
+                            os.path.join(ROOT, "include"), str(src)], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+
+
+def test_library_exports_every_declared_symbol():
+    L = lmx.lib()
+    names = declared_functions()
+    assert len(names) == 11
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(lmx.SIGNATURES)
+    out = subprocess.run(["nm", "-D", "--defined-only", lmx.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (lmx_\w+)", out))
+    assert exported == set(names)
+
+
+def test_status_strings_and_version():
+    L = lmx.lib()
+    assert L.lmx_version() == 100
+    for s in lmx.Status:
+        assert L.lmx_status_str(int(s))
+    assert L.lmx_status_str(999) == b"unknown status"
+
+
+def _params(**kw):
+    base = dict(n_tokens=1, n_heads=32, n_kv_heads=8, head_dim=128, base_pos=0, n_slots=16)
+    base.update(kw)
+    return lmx.attn_params(**base)
+
+
+FAKE = 0x100000  # never dereferenced: validation fails first
+
+
+def _fwd(p, q=FAKE, k=FAKE, v=FAKE, out=FAKE, kc=None, vc=None, qdt=lmx.F32, kvdt=lmx.F16):
+    return lmx.lib().lmx_attn_fwd(ctypes.byref(p), q, qdt, k, v, kvdt, kc, vc, out, None, 0, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n_tokens=0), lmx.Status.E_SHAPE),
+    (dict(n_heads=30), lmx.Status.E_SHAPE),
+    (dict(head_dim=96), lmx.Status.E_UNSUPPORTED),
+    (dict(kv_dim=512), lmx.Status.E_SHAPE),
+    (dict(base_pos=16), lmx.Status.E_CONTEXT),
+    (dict(n_tokens=17), lmx.Status.E_CONTEXT),
+    (dict(window=32, n_slots=16), lmx.Status.E_SHAPE),
+    (dict(scale=float("nan")), lmx.Status.E_SHAPE),
+    (dict(window=16, n_tokens=12, base_pos=8), lmx.Status.E_RING_HAZARD),
+])
+def test_attn_fwd_rejects_bad_geometry(kw, code):
+    assert _fwd(_params(**kw)) == code
+
+
+def test_attn_fwd_rejects_bad_pointers_and_dtypes():
+    p = _params()
+    assert _fwd(p, q=None) == lmx.Status.E_NULL
+    assert _fwd(p, out=None) == lmx.Status.E_NULL
+    assert _fwd(p, kc=FAKE) == lmx.Status.E_NULL  # k_cur without v_cur
+    assert _fwd(p, q=FAKE + 2) == lmx.Status.E_ALIGN
+    assert _fwd(p, kvdt=lmx.F32) == lmx.Status.E_UNSUPPORTED
+    assert _fwd(p, qdt=7) == lmx.Status.E_UNSUPPORTED
+    assert lmx.lib().lmx_attn_fwd(None, FAKE, 0, FAKE, FAKE, 1, None, None, FAKE, None, 0, None) == lmx.Status.E_NULL
+
+
+def test_decode_needs_workspace_when_split():
+    p = _params(n_slots=32768, base_pos=32767)
+    need = lmx.lib().lmx_attn_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    assert _fwd(p) == lmx.Status.E_WORKSPACE
+    # no split at tiny context: no workspace
+    assert lmx.lib().lmx_attn_workspace_bytes(ctypes.byref(_params(n_slots=16, base_pos=3))) == 0
+
+
+def test_workspace_bytes_is_zero_for_invalid_params():
+    assert lmx.lib().lmx_attn_workspace_bytes(ctypes.byref(_params(n_heads=31))) == 0
+    assert lmx.lib().lmx_attn_workspace_bytes(None) == 0
+
+
+def test_kv_append_validation():
+    L = lmx.lib()
+    d = lmx.KvDesc(4, 1024, 10, 0, 12)
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, lmx.F16, None) == lmx.Status.E_CONTEXT
+    d = lmx.KvDesc(4, 1022, 0, 0, 12)
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, lmx.F16, None) == lmx.Status.E_SHAPE
+    d = lmx.KvDesc(4, 1024, 0, 0, 12)
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE, None, FAKE, FAKE, lmx.F16, None) == lmx.Status.E_NULL
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, lmx.F32, None) == lmx.Status.E_UNSUPPORTED
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE + 4, FAKE, FAKE, FAKE, lmx.F16, None) == lmx.Status.E_ALIGN
+    d = lmx.KvDesc(4, 1024, 0, 8, 4)
+    assert L.lmx_kv_append(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, lmx.F16, None) == lmx.Status.E_SHAPE
+
+
+def test_batched_validation():
+    L = lmx.lib()
+    p = _params(n_slots=1024)
+    call = lambda p, n, mx, **kw: L.lmx_attn_decode_batched(
+        ctypes.byref(p), n, mx, kw.get("ctx", FAKE), FAKE, FAKE, FAKE, lmx.F32, lmx.F16, FAKE, None, 0, None)
+    assert call(p, 0, 100) == lmx.Status.E_SHAPE
+    assert call(p, 4, 2000) == lmx.Status.E_CONTEXT
+    assert call(_params(n_tokens=2, n_slots=1024), 4, 100) == lmx.Status.E_SHAPE
+    assert call(p, 4, 100, ctx=None) == lmx.Status.E_NULL
+    assert L.lmx_attn_decode_batched_workspace_bytes(ctypes.byref(p), 32, 1024) > 0
+
+
+def test_deltanet_validation():
+    L = lmx.lib()
+    op = lmx.dop(n_tok=4, n_vh=32, n_kh=16, s_dim=128)
+    args = [FAKE] * 7
+    assert L.lmx_deltanet_recur(ctypes.byref(op), *args[:5], None, FAKE, None) == lmx.Status.E_NULL
+    bad = lmx.dop(n_tok=4, n_vh=32, n_kh=16, s_dim=96)
+    assert L.lmx_deltanet_recur(ctypes.byref(bad), *args, None) == lmx.Status.E_UNSUPPORTED
+    bad = lmx.dop(n_tok=0, n_vh=32, n_kh=16, s_dim=128)
+    assert L.lmx_deltanet_recur(ctypes.byref(bad), *args, None) == lmx.Status.E_SHAPE
+    op2 = lmx.dop(n_tok=4, n_vh=32, n_kh=16, s_dim=128)
+    op2.key_dim = 100
+    assert L.lmx_deltanet_recur(ctypes.byref(op2), *args, None) == lmx.Status.E_SHAPE
+    assert L.lmx_deltanet_chunked(ctypes.byref(op), *args, 48, None, 0, None) == lmx.Status.E_SHAPE
+    assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), 48) == 0

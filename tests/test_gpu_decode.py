@@ -1,0 +1,126 @@
+"""GPU parity: split-K decode attention (few query tokens) vs the C oracle.
+
+Tolerance: max abs error <= 2e-3 and max|diff|/max|ref| <= 1e-2 on the fp32
+outputs (tests/helpers.py), with f16 K/V and the oracle reading the identical
+f16 values upcast to f32.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests.helpers import AttnCase, assert_close
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import llmoxide_amd as lmx  # noqa: E402
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.cuda()
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run_case(c: AttnCase, *, base, window=0, bidi=False, scale=None, ring=False, k_cur=False):
+    say(f"case t={c.t} H={c.H} Hkv={c.Hkv} hd={c.hd} base={base} w={window} bidi={bidi} "
+        f"ring={ring} k_cur={k_cur} q_f16={c.q_f16}")
+    end = base + c.t
+    if ring:
+        kc, vc = c.ring(window, end if not k_cur else base)
+    else:
+        kc, vc = c.k16[:end], c.v16[:end]
+    q = dev(c.q.astype(np.float16)) if c.q_f16 else dev(c.q)
+    kw = {}
+    if k_cur:
+        kw = dict(k_cur=dev(c.k16[base:end], torch.float16), v_cur=dev(c.v16[base:end], torch.float16))
+    out = lmx.attention(q, dev(kc, torch.float16), dev(vc, torch.float16), n_heads=c.H,
+                        n_kv_heads=c.Hkv, head_dim=c.hd, base_pos=base, window=window, bidi=bidi,
+                        scale=scale, kv_dim=c.kv_dim, **kw)
+    torch.cuda.synchronize()
+    ref = c.reference(base_pos=base, window=window, bidi=bidi, scale=scale)
+    return assert_close(out.cpu().numpy(), ref, what="decode")
+
+
+def test_c1_config():
+    """C1: H=16, Hkv=8, hd=128, 512 cached tokens, query at pos 511, f32 Q."""
+    c = AttnCase(1, t=1, H=16, Hkv=8, hd=128, n_pos=512)
+    run_case(c, base=511)
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 63, 64, 65, 257, 1000, 4097, 12345, 32768])
+def test_qwen3_8b_shape_decode(ctx):
+    c = AttnCase(ctx, t=1, H=32, Hkv=8, hd=128, n_pos=ctx)
+    run_case(c, base=ctx - 1)
+
+
+def test_f16_query():
+    c = AttnCase(3, t=1, H=32, Hkv=8, hd=128, n_pos=3000, q_f16=True)
+    run_case(c, base=2999)
+
+
+@pytest.mark.parametrize("H,Hkv,hd", [(8, 8, 128), (16, 2, 128), (24, 4, 128), (16, 1, 64),
+                                      (8, 2, 64), (16, 8, 256), (4, 1, 512), (16, 1, 512)])
+def test_head_geometries(H, Hkv, hd):
+    c = AttnCase(H * 7 + hd, t=1, H=H, Hkv=Hkv, hd=hd, n_pos=2500)
+    run_case(c, base=2499, scale=1.0 / np.sqrt(hd))
+
+
+def test_padded_kv_rows():
+    c = AttnCase(8, t=1, H=8, Hkv=2, hd=128, n_pos=700, kv_dim=2 * 128 + 64)
+    run_case(c, base=699)
+
+
+@pytest.mark.parametrize("window,ctx", [(4, 37), (7, 1000), (1024, 1500), (1024, 32768), (100, 100)])
+def test_ring_window_decode(window, ctx):
+    """Sliding-window decode from a ring cache (Gemma SWA layers, scale 1/16)."""
+    c = AttnCase(window + ctx, t=1, H=16, Hkv=8, hd=256, n_pos=ctx)
+    run_case(c, base=ctx - 1, window=window, scale=1.0 / 16, ring=True)
+
+
+@pytest.mark.parametrize("t,base", [(2, 0), (5, 300), (8, 4095)])
+def test_few_tokens_causal(t, base):
+    c = AttnCase(t + base, t=t, H=32, Hkv=8, hd=128, n_pos=base + t)
+    run_case(c, base=base)
+
+
+@pytest.mark.parametrize("window", [0, 3, 16])
+def test_few_tokens_bidi(window):
+    c = AttnCase(40 + window, t=6, H=8, Hkv=2, hd=64, n_pos=50)
+    run_case(c, base=44, window=window, bidi=True, k_cur=bool(window), ring=bool(window))
+
+
+def test_windowed_batch_with_k_cur():
+    """A windowed batch past the ring's self-consistent regime reads its own
+    rows from k_cur/v_cur and earlier positions from the ring."""
+    c = AttnCase(91, t=7, H=8, Hkv=4, hd=128, n_pos=60)
+    run_case(c, base=53, window=16, ring=True, k_cur=True)
+
+
+def test_ring_hazard_is_refused():
+    c = AttnCase(92, t=7, H=8, Hkv=4, hd=128, n_pos=60)
+    kc, vc = c.ring(16, 60)
+    with pytest.raises(lmx.LmxError) as e:
+        lmx.attention(dev(c.q), dev(kc, torch.float16), dev(vc, torch.float16), n_heads=8,
+                      n_kv_heads=4, head_dim=128, base_pos=53, window=16)
+    assert e.value.status == lmx.Status.E_RING_HAZARD
+
+
+def test_repeat_calls_reuse_workspace():
+    """Counters are left at zero, so back-to-back calls on one workspace agree."""
+    c = AttnCase(17, t=1, H=32, Hkv=8, hd=128, n_pos=20000)
+    ws = lmx.Workspace()
+    q = dev(c.q)
+    kc, vc = dev(c.k16, torch.float16), dev(c.v16, torch.float16)
+    outs = [lmx.attention(q, kc, vc, n_heads=32, n_kv_heads=8, head_dim=128, base_pos=19999,
+                          workspace=ws).cpu().numpy() for _ in range(5)]
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    assert_close(outs[0], c.reference(base_pos=19999))

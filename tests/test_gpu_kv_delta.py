@@ -1,0 +1,131 @@
+"""GPU parity: KV append (bit-exact f16 rows and slots), the token-sequential
+and chunked delta rule, and ragged multi-sequence decode."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import AttnCase, assert_close, delta_inputs
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import llmoxide_amd as lmx  # noqa: E402
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.cuda()
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ---------------------------------------------------------------- kv append --
+@pytest.mark.parametrize("window,base,t,n_slots", [
+    (0, 0, 1, 8), (0, 5, 17, 40), (0, 4096, 512, 4608),
+    (8, 0, 5, 8), (8, 6, 5, 8), (8, 3, 21, 8), (1024, 1000, 4096, 1024),
+])
+def test_kv_append_matches_write_cache(window, base, t, n_slots):
+    say(f"kv_append w={window} base={base} t={t} slots={n_slots}")
+    kv_dim = 1024
+    k = oracle.normal(window + base + t, (t, kv_dim)) * np.float32(3.0)
+    v = oracle.normal(window + base + t + 1, (t, kv_dim))
+    init = np.full((n_slots, kv_dim), 0x3C00, np.uint16)  # 1.0 everywhere
+    ek, ev = init.copy(), init.copy()
+    oracle.write_cache(k, ek, base, window)
+    oracle.write_cache(v, ev, base, window)
+    kc, vc = dev(init, torch.float16), dev(init, torch.float16)
+    lmx.write_cache(dev(k), dev(v), kc, vc, base_pos=base, window=window)
+    torch.cuda.synchronize()
+    assert np.array_equal(kc.cpu().view(torch.int16).numpy().view(np.uint16), ek)
+    assert np.array_equal(vc.cpu().view(torch.int16).numpy().view(np.uint16), ev)
+
+
+def test_append_then_decode_matches_reference_cache_path():
+    """write_cache then attention, decode step by step, equals the oracle."""
+    H, Hkv, hd, n = 8, 2, 128, 40
+    c = AttnCase(55, t=n, H=H, Hkv=Hkv, hd=hd, n_pos=n)
+    kc = torch.zeros((n, Hkv * hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    for pos in range(n):
+        lmx.write_cache(dev(c.kf[pos:pos + 1]), dev(c.vf[pos:pos + 1]), kc, vc, base_pos=pos)
+        out = lmx.attention(dev(c.q[pos:pos + 1]), kc, vc, n_heads=H, n_kv_heads=Hkv, head_dim=hd,
+                            base_pos=pos)
+        ref = oracle.attention(c.q[pos:pos + 1], c.kf, c.vf, n_heads=H, n_kv_heads=Hkv, head_dim=hd,
+                               base_pos=pos)
+        assert_close(out.cpu().numpy(), ref, what=f"pos {pos}")
+
+
+# -------------------------------------------------------------- delta rule --
+def _delta_gpu(fn, conv, al, be, S0, A, dt, n_vh, n_kh, sd, **kw):
+    state = dev(S0.copy())
+    out = fn(dev(conv), dev(al), dev(be), state, dev(A), dev(dt), n_vh=n_vh, n_kh=n_kh, s_dim=sd, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), state.cpu().numpy()
+
+
+@pytest.mark.parametrize("n_vh,n_kh,sd,T,s0", [(4, 2, 64, 37, 0.0), (4, 2, 64, 5, 0.5),
+                                               (32, 16, 128, 64, 0.0), (32, 16, 128, 1, 0.3),
+                                               (6, 3, 128, 130, 0.1)])
+def test_delta_recur(n_vh, n_kh, sd, T, s0):
+    say(f"delta_recur n_vh={n_vh} n_kh={n_kh} sd={sd} T={T} s0={s0}")
+    conv, al, be, S0, A, dt = delta_inputs(T + n_vh, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=s0)
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    o, S = _delta_gpu(lmx.delta_recur, conv, al, be, S0, A, dt, n_vh, n_kh, sd)
+    assert_close(o, o_ref, what="o")
+    assert_close(S, S_ref, what="S")
+
+
+@pytest.mark.parametrize("T,chunk", [(37, 16), (64, 64), (200, 64), (256, 32)])
+def test_delta_chunked_matches_sequential(T, chunk):
+    n_vh, n_kh, sd = 8, 4, 128
+    say(f"delta_chunked T={T} chunk={chunk}")
+    conv, al, be, S0, A, dt = delta_inputs(T + 7, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.2)
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    o, S = _delta_gpu(lmx.delta_chunked, conv, al, be, S0, A, dt, n_vh, n_kh, sd, chunk=chunk)
+    assert_close(o, o_ref, what="o")
+    assert_close(S, S_ref, what="S")
+
+
+# ------------------------------------------------------- ragged batch decode --
+def _batched(B, lens, H=32, Hkv=8, hd=128, seed=0, q_f16=False):
+    say(f"batched B={B} lens={lens}")
+    cases = [AttnCase(seed + i, t=1, H=H, Hkv=Hkv, hd=hd, n_pos=int(n), q_f16=q_f16)
+             for i, n in enumerate(lens)]
+    max_ctx = int(max(lens))
+    ks = [dev(np.pad(c.k16, ((0, max_ctx - c.n_pos), (0, 0))), torch.float16) for c in cases]
+    vs = [dev(np.pad(c.v16, ((0, max_ctx - c.n_pos), (0, 0))), torch.float16) for c in cases]
+    q = np.concatenate([c.q for c in cases])
+    qd = dev(q.astype(np.float16)) if q_f16 else dev(q)
+    caches = lmx.BatchedCaches(ks, vs)
+    ctx = dev(np.array(lens, np.int32))
+    out = lmx.attention_decode_batched(qd, caches, ctx, max_ctx=max_ctx, n_heads=H, n_kv_heads=Hkv,
+                                       head_dim=hd)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for i, c in enumerate(cases):
+        assert_close(out[i:i + 1], c.reference(base_pos=c.n_pos - 1), what=f"seq {i}")
+    return out, cases, ks, vs
+
+
+def test_batched_ragged_b8():
+    rng = np.random.default_rng(8)
+    _batched(8, rng.integers(1024, 32769, 8).tolist(), seed=100)
+
+
+def test_batched_small_and_f16_query():
+    _batched(5, [1, 2, 64, 65, 700], seed=200, q_f16=True)
+
+
+def test_batched_single_sequence_equals_attn_fwd():
+    out, cases, ks, vs = _batched(1, [5000], seed=300)
+    c = cases[0]
+    single = lmx.attention(dev(c.q), ks[0], vs[0], n_heads=32, n_kv_heads=8, head_dim=128,
+                           base_pos=4999)
+    assert np.array_equal(single.cpu().numpy(), out)
