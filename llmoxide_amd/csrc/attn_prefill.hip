@@ -1,14 +1,304 @@
-// Placeholder: the MFMA prefill kernel is not in yet; every batch takes the
-// split-K path.
+// Tiled attention for long batches (prefill) on gfx950 MFMA.
+//
+// Replaces, for n_tokens large, the reference's scores_pass / softmax_pass /
+// weighted_v (attn.wgsl:84-232), which materialize an f32 [t, H, max_vis]
+// scores buffer in HBM.  Here scores stay in registers:
+//
+//   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q rows
+//                 held in registers for the whole key loop
+//   online softmax in fp32 (exp2 with scale*log2e folded in), P rounded to f16
+//   O^T += V^T P^T  A = V^T from a transposed LDS tile, B = P straight from the
+//                 S^T accumulators (no shuffle: computing the transpose makes
+//                 each lane own one query column, so softmax is mostly in-lane)
+//
+// Workgroup = 4 waves x 32 query rows of one query head; K/V tiles of 64 keys
+// are staged in LDS.  Key tiles outside a wave's visible range are skipped
+// (causal / window), tiles inside every query's range skip the mask.
+// Workgroups are ordered so each XCD owns whole kv heads (its L2 serves the
+// G query heads that share them) and heavy causal tiles start first.
+#include <climits>
+
 #include "common.hpp"
 
 namespace lmx {
 
-bool prefill_supported(const lmx_attn_params*, lmx_dtype) { return false; }
+struct PrefillArgs {
+    const void* q;
+    const f16* k;
+    const f16* v;
+    const f16* k_cur;
+    const f16* v_cur;
+    float* out;
+    int H, Hkv, G, kv_dim;
+    int base_pos, window, n_tokens, bidi;
+    int n_qtiles;
+    float c;  // scale * log2(e)
+};
 
-lmx_status prefill_fwd(const lmx_attn_params*, const void*, lmx_dtype, const void*, const void*,
-                       const void*, const void*, float*, hipStream_t) {
-    return LMX_E_UNSUPPORTED;
+constexpr int kPfBM = 128;  // query rows per workgroup
+constexpr int kPfBN = 64;   // keys per LDS tile
+
+// attn.wgsl:52-66
+__device__ __forceinline__ int vis_lo(int pos, int w) { return (w && pos + 1 > w) ? pos + 1 - w : 0; }
+__device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
+    if (!bidi) return pos;
+    return w ? min(end, pos + w - 1) : end;
+}
+
+// Bijective block remap so that consecutive logical ids share an XCD (blocks
+// are dispatched round-robin over 8 XCDs).
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+    const int q = n / 8, r = n % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+template <typename QT, int HD>
+__global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int BN = kPfBN;
+    constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
+    constexpr int NB = HD / 32;      // 32-dim output blocks
+    constexpr int KPAD = HD + 8;     // K_s row stride (halfs)
+    constexpr int VPAD = BN + 4;     // Vt_s row stride (halfs), 8-byte aligned rows
+    __shared__ __attribute__((aligned(16))) f16 K_s[BN * KPAD];
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[HD * VPAD];
+
+    // ---- which (head, query tile) this workgroup owns
+    const int nblk = gridDim.x;
+    const int logical = xcd_remap(blockIdx.x, nblk);
+    const int per_kvh = a.n_qtiles * a.G;
+    const int kvh = logical / per_kvh;
+    const int rem = logical - kvh * per_kvh;
+    const int qt = a.n_qtiles - 1 - rem / a.G;
+    const int h = kvh * a.G + (rem % a.G);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int t = a.n_tokens, base = a.base_pos, w = a.window;
+    const int end = base + t - 1;
+    const int q0 = qt * kPfBM;
+    const int qw0 = q0 + wave * 32;
+
+    // ---- this lane's query (column l32 of the wave's S^T tiles)
+    const int qrow = qw0 + l32;
+    const bool qvalid = qrow < t;
+    const int qpos = base + qrow;
+    const int my_lo = qvalid ? vis_lo(qpos, w) : 1;
+    const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
+
+    // Q as the B operand: lane holds Q[qrow][ks*16 + 8*hh + j], j < 8.
+    f16x8 qf[KSTEPS];
+    {
+        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * HD + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            if constexpr (sizeof(QT) == 2) {
+                qf[ks] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qoff + ks * 16);
+            } else {
+                const float* qp = reinterpret_cast<const float*>(a.q) + qoff + ks * 16;
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
+                qf[ks] = f16x8{(f16)x0[0], (f16)x0[1], (f16)x0[2], (f16)x0[3],
+                               (f16)x1[0], (f16)x1[1], (f16)x1[2], (f16)x1[3]};
+            }
+        }
+    }
+
+    // ---- key ranges: the workgroup's, and this wave's
+    const int q_last = min(q0 + kPfBM, t) - 1;
+    const int wg_lo = vis_lo(base + q0, w);
+    const int wg_hi = vis_hi(base + q_last, w, a.bidi, end);
+    const int wq_last = min(qw0 + 31, t - 1);
+    const bool wave_live = qw0 < t;
+    const int wv_lo = wave_live ? vis_lo(base + qw0, w) : 1;                    // smallest lo
+    const int wv_hi = wave_live ? vis_hi(base + wq_last, w, a.bidi, end) : 0;  // largest hi
+    const int wv_lo_max = wave_live ? vis_lo(base + wq_last, w) : 0;          // largest lo
+    const int wv_hi_min = wave_live ? vis_hi(base + qw0, w, a.bidi, end) : -1; // smallest hi
+
+    const int cur_begin = a.k_cur ? base : INT_MAX;
+
+    float m_run = -1e30f, l_run = 0.f;
+    f32x16 o[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[nb][i] = 0.f;
+
+    const int kt_begin = (wg_lo / BN) * BN;
+    for (int kt = kt_begin; kt <= wg_hi; kt += BN) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        // ---- K tile -> K_s[key][dim]; rows outside [wg_lo, wg_hi] are zero
+        constexpr int KCH = HD / 8;  // 16-byte chunks per key row
+        for (int c = tid; c < BN * KCH; c += 256) {
+            const int key = c / KCH, col = c - key * KCH;
+            const int p = kt + key;
+            f16x8 val = {};
+            if (p >= wg_lo && p <= wg_hi) {
+                const f16* src;
+                if (p >= cur_begin) {
+                    src = a.k_cur + (size_t)(p - base) * a.kv_dim;
+                } else {
+                    const int s = w ? p % w : p;
+                    src = a.k + (size_t)s * a.kv_dim;
+                }
+                val = *reinterpret_cast<const f16x8*>(src + kvh * HD + col * 8);
+            }
+            *reinterpret_cast<f16x8*>(&K_s[key * KPAD + col * 8]) = val;
+        }
+        // ---- V tile -> Vt_s[dim][key] (transposed), four keys per 8-byte write
+        for (int pr = tid; pr < KCH * (BN / 4); pr += 256) {
+            const int dc = pr % KCH, kg = pr / KCH;
+            f16x8 r[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int p = kt + 4 * kg + u;
+                r[u] = f16x8{};
+                if (p >= wg_lo && p <= wg_hi) {
+                    const f16* src;
+                    if (p >= cur_begin) {
+                        src = a.v_cur + (size_t)(p - base) * a.kv_dim;
+                    } else {
+                        const int s = w ? p % w : p;
+                        src = a.v + (size_t)s * a.kv_dim;
+                    }
+                    r[u] = *reinterpret_cast<const f16x8*>(src + kvh * HD + dc * 8);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<f16x4*>(&Vt_s[(dc * 8 + j) * VPAD + 4 * kg]) =
+                    f16x4{r[0][j], r[1][j], r[2][j], r[3][j]};
+        }
+        __syncthreads();
+
+        if (!wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
+        const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
+
+        // ---- S^T = K Q^T, two 32-key blocks
+        f32x16 s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
+            const f16* krow = &K_s[(kb * 32 + l32) * KPAD + 8 * hh];
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + ks * 16);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[ks], s[kb], 0, 0, 0);
+            }
+        }
+
+        // ---- scale, mask, online softmax.  s[kb][i] is key
+        //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow.
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float x = s[kb][i] * a.c;
+                if (need_mask) {
+                    const int key = kt + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                    if (key < my_lo || key > my_hi) x = -INFINITY;
+                }
+                s[kb][i] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float mn = fmaxf(m_run, mt);
+        const float corr = fast_exp2(m_run - mn);
+        m_run = mn;
+        l_run *= corr;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+
+        // P^T as the B operand of 4 k-steps (16 keys each): step st takes
+        // registers 8*(st%2) .. +7 of s[st/2].
+        f16x8 pf[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = fast_exp2(s[st / 2][8 * (st % 2) + j] - mn);
+                l_run += p;
+                pf[st][j] = (f16)p;
+            }
+
+        // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
+        //      16*st' + 4*hh + {0..3} and 16*st' + 8 + 4*hh + {0..3} of the tile.
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const f16* vrow = &Vt_s[(nb * 32 + l32) * VPAD + 4 * hh];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
+                const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
+                const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[st], o[nb], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- normalize and store: o[nb][i] is dim nb*32 + 8*(i/4) + 4*hh + i%4
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    if (!qvalid) return;
+    const float inv = 1.f / l_tot;
+    float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+            *reinterpret_cast<f32x4*>(orow + nb * 32 + 8 * g4 + 4 * hh) =
+                f32x4{o[nb][4 * g4] * inv, o[nb][4 * g4 + 1] * inv, o[nb][4 * g4 + 2] * inv,
+                      o[nb][4 * g4 + 3] * inv};
+}
+
+bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
+    (void)q_dt;
+    return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
+}
+
+lmx_status prefill_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
+                       const void* v_cache, const void* k_cur, const void* v_cur, float* out,
+                       hipStream_t st) {
+    PrefillArgs a{};
+    a.q = q;
+    a.k = static_cast<const f16*>(k_cache);
+    a.v = static_cast<const f16*>(v_cache);
+    a.k_cur = static_cast<const f16*>(k_cur);
+    a.v_cur = static_cast<const f16*>(v_cur);
+    a.out = out;
+    a.H = (int)p->n_heads;
+    a.Hkv = (int)p->n_kv_heads;
+    a.G = a.H / a.Hkv;
+    a.kv_dim = (int)p->kv_dim;
+    a.base_pos = (int)p->base_pos;
+    a.window = (int)p->window;
+    a.n_tokens = (int)p->n_tokens;
+    a.bidi = (int)p->bidi;
+    a.c = p->scale * kLog2e;
+    a.n_qtiles = (a.n_tokens + kPfBM - 1) / kPfBM;
+    const long nblk = (long)a.n_qtiles * a.H;
+    if (nblk > INT_MAX) return LMX_E_SHAPE;
+    dim3 grid((unsigned)nblk);
+    (void)hipGetLastError();
+    const int hd = (int)p->head_dim;
+#define LMX_PF(QT, HDV) hipLaunchKernelGGL((attn_prefill_kernel<QT, HDV>), grid, dim3(256), 0, st, a)
+    if (q_dt == LMX_F16) {
+        if (hd == 64) LMX_PF(f16, 64);
+        else if (hd == 128) LMX_PF(f16, 128);
+        else if (hd == 256) LMX_PF(f16, 256);
+        else return LMX_E_UNSUPPORTED;
+    } else {
+        if (hd == 64) LMX_PF(float, 64);
+        else if (hd == 128) LMX_PF(float, 128);
+        else if (hd == 256) LMX_PF(float, 256);
+        else return LMX_E_UNSUPPORTED;
+    }
+#undef LMX_PF
+    LMX_CHECK_LAUNCH();
+    return LMX_OK;
 }
 
 }  // namespace lmx
