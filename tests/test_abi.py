@@ -125,7 +125,9 @@ def test_batched_validation():
     assert call(p, 4, 2000) == lmx.Status.E_CONTEXT
     assert call(_params(n_tokens=2, n_slots=1024), 4, 100) == lmx.Status.E_SHAPE
     assert call(p, 4, 100, ctx=None) == lmx.Status.E_NULL
-    assert L.lmx_attn_decode_batched_workspace_bytes(ctypes.byref(p), 32, 1024) > 0
+    # one long sequence is split over many workgroups and needs partials
+    big = _params(n_slots=32768)
+    assert L.lmx_attn_decode_batched_workspace_bytes(ctypes.byref(big), 1, 32768) > 0
 
 
 def test_deltanet_validation():
