@@ -4,32 +4,44 @@
 // softmax_pass / weighted_v (attn.wgsl:84-232), which give decode only
 // n_heads workgroups and a serial key loop (attn.wgsl:13-17).
 //
-// Work split.  A "unit" is one (query, kv head, block of GB query heads that
-// share the kv head); K/V of a unit are read once for all GB heads (GQA).  A
-// unit's visible key range is cut into chunks of kWaves*kTU*16 keys; P
-// workgroups serve each unit, workgroup w taking chunks w, w+P, w+2P, ...
-// (a static, deterministic split).  Every wave streams its share of those
-// chunks with the next chunk's K/V loads in flight while it computes the
-// current one.  Each workgroup leaves one partial (max, sum, o[hd]) per head;
-// the last workgroup to arrive merges the unit's partials.  Partials cross workgroups with
-// agent-coherent (sc1) stores and loads and a counter atomic issued after the
-// stores are acknowledged, so no L2 writeback is needed.
+// Work split.  A workgroup owns HW kv heads (one wave group per head) for a
+// block of GB query heads per kv head, one query row, and split s of the
+// visible keys: the contiguous 16-key tiles [s*tps, (s+1)*tps).  With HW = 8
+// and one wave per head, the workgroup's loads cover whole cache rows (a
+// row holds every kv head), which is the access pattern HBM serves fastest;
+// K/V rows are read once for all GB query heads of a kv head (GQA) and with
+// non-temporal loads (they are streamed, never re-read).  Each wave keeps
+// two tiles of K/V in registers: while it computes one, the next one's loads
+// are in flight.  Row addressing is branch-free: a linear cache reads row p,
+// a ring reads slot p % window (multiply-high division), and rows of the
+// current batch can come from a separate k_cur/v_cur buffer.
 //
-// Per wave, 16-key tiles:
+// Per wave and tile:
 //   S^T[16 keys x 16 cols] = K Q^T on v_mfma_f32_16x16x32_f16.  Columns
 //   0..GB-1 hold the f16 high part of each query head, columns GB..2GB-1 the
 //   f16 residual (q - hi) of an fp32 query, so q.k is exact to ~2^-22.
-//   Lane (g, c) then holds keys 4g..4g+3 of column c: the online softmax runs
-//   once per (key, head), in fp32, with exp2 and scale*log2(e) folded in.
-//   p goes through a small per-wave LDS slot to the P.V lanes, which own
-//   hd/16 dims of one key in four and accumulate in fp32 VALU (each lane reads
-//   a contiguous hd/16-element slice of a V row).
+//   Lane (g, c) then holds keys 4g..4g+3 of column c.  Each 16-lane group g
+//   runs its own online softmax over its four keys of every tile (fp32, exp2
+//   with scale*log2(e) folded in), so no value crosses groups inside the
+//   loop; the four streams are merged once at the end.  p goes through a
+//   per-wave LDS slot to the P.V lanes of the same group; those read V rows
+//   coalesced (16 lanes cover one 256-byte row) and accumulate in fp32.
+//
+// Merge.  With one split per unit the workgroup writes the output.  Else
+// each split workgroup stores one partial (max, sum, o[hd]) per query head
+// and a second, small kernel merges them: each of its threads folds up to
+// eight partials of one float4 column (all loads issued at once), and the
+// parts of a column are combined in an LDS tree.  The launch boundary
+// orders the partial stores before the merge loads; no counters, so the
+// pair can be replayed from a captured graph as is.
 #include <climits>
 #include <cstdlib>
 
 #include "common.hpp"
 
 namespace lmx {
+
+enum DecodeMode { kModeLinear = 0, kModeGeneral = 1, kModeBatched = 2 };
 
 struct DecodeArgs {
     const void* q;
@@ -41,41 +53,46 @@ struct DecodeArgs {
     const f16* v_cur;
     const int32_t* ctx_lens;
     float* out;
-    float* part_o;          // [n_q][H][P][HD]   per-workgroup partials
-    float* part_ml;         // [n_q][H][P][2]    (max in log2 units, sum)
-    uint32_t* ctr_arrive;   // [units]  workgroups finished
+    float* part_o;          // [n_q][H][P][HD]  per-split partials
+    float* part_ml;         // [n_q][H][P][2]   (max in log2 units, sum)
     int H, Hkv, G, kv_dim;
     int base_pos, window, n_tokens, bidi;
-    int P, n_hblk;
-    int max_ctx;  // batched: context lengths are clamped to [1, max_ctx]
-    float c;      // scale * log2(e)
+    int P, tps, n_hblk;
+    int n_q;                // query rows (tokens, or sequences when batched)
+    int n_main, n_yg;       // split workgroups; their (kv group, head block) count
+    int n_merge, m_cols, m_parts, m_heads, m_slices;  // merge workgroup layout
+    int max_ctx;            // batched: context lengths are clamped to [1, max_ctx]
+    uint32_t w_magic;       // p % window == p - window * ((p * w_magic) >> w_shift)
+    int w_shift;
+    float c;                // scale * log2(e)
 };
 
 constexpr int kWaves = 8;
 constexpr int kDecThreads = kWaves * 64;
-constexpr int kMaxP = 64;  // workgroups per unit
+constexpr int kMaxP = 512;  // splits per unit
+constexpr int kTile = 16;   // keys per wave tile
+constexpr int kMergePer = 8;            // partials per merge thread
 
-// Register budget per lane (of 256 at two waves per SIMD) for the K/V tile
-// buffers: each 16-key tile holds hd/8 VGPRs of K and hd/8 of V per lane.
-// Two tiles per wave per chunk, double-buffered, when they fit; else one tile,
-// double-buffered; else one tile, loaded and used in turn.
-__host__ __device__ constexpr int dec_base_regs(int hd, int gb) { return hd / 8 + gb * hd / 16 + 48; }
-__host__ __device__ constexpr int dec_tile_regs(int hd) { return hd / 8 + hd / 8; }
-__host__ __device__ constexpr int tiles_per_wave(int hd, int gb) {
-    return dec_base_regs(hd, gb) + 4 * dec_tile_regs(hd) <= 232 ? 2 : 1;
-}
-__host__ __device__ constexpr bool dec_pipelined(int hd, int gb) {
-    return dec_base_regs(hd, gb) + 2 * tiles_per_wave(hd, gb) * dec_tile_regs(hd) <= 232;
-}
-__host__ __device__ constexpr int chunk_keys(int hd, int gb) { return kWaves * tiles_per_wave(hd, gb) * 16; }
-
-// Agent-coherent accesses (global_store/load ... sc1): visible across XCDs
-// without an L2 writeback.
-__device__ __forceinline__ void st_co(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_co(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
+// batched: the sequence's last position).
+template <int MODE>
+__device__ __forceinline__ void unit_range(const DecodeArgs& a, int qi, int& lo, int& hi) {
+    int pos;
+    if constexpr (MODE == kModeBatched) {
+        // Out-of-range lengths are clamped so every read stays in the cache
+        // the caller sized for max_ctx.
+        pos = min(max(a.ctx_lens[qi], 1), a.max_ctx) - 1;
+        hi = pos;
+    } else {
+        pos = a.base_pos + qi;
+        if (a.bidi) {
+            const int end = a.base_pos + a.n_tokens - 1;
+            hi = a.window ? min(end, pos + a.window - 1) : end;
+        } else {
+            hi = pos;
+        }
+    }
+    lo = (a.window && pos + 1 > a.window) ? pos + 1 - a.window : 0;
 }
 
 // Order LDS traffic between lanes of one wave (LDS executes a wave's
@@ -92,379 +109,498 @@ __device__ __forceinline__ float row_rotate_down(float x) {
     return dpp<0x120 + (16 - N)>(x);  // row_ror:(16-N)
 }
 
-template <typename QT, int HD, int GB, bool BATCHED>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) {
-    constexpr int KD = HD / 4;      // K dims per lane (contiguous)
-    constexpr int KSTEP = HD / 32;  // MFMA k-steps
-    constexpr int DPL = HD / 16;    // V dims per lane
-    constexpr bool SPLIT_Q = sizeof(QT) == 4;
-    constexpr int kTU = tiles_per_wave(HD, GB);
-    constexpr int CH = chunk_keys(HD, GB);
-    constexpr bool PIPE = dec_pipelined(HD, GB);
-    static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
-    const int wg = blockIdx.x;
-    const int kvh = blockIdx.y / a.n_hblk;
-    const int hb = blockIdx.y - kvh * a.n_hblk;
-    const int qi = blockIdx.z;
-    const int h0 = kvh * a.G + hb * GB;
-    const size_t unit = ((size_t)qi * a.Hkv + kvh) * a.n_hblk + hb;
+// Per-lane K/V registers of one 16-key tile.
+//  K (MFMA A operand): lane (key c16, group g4), k-step s holds dims
+//    32s + 8g4 .. +7 of key c16: each load covers 64 contiguous bytes per key.
+//  V (P.V operand): load i, lane (g4, c16) holds key 4g4 + i, dims
+//    128r + 8c16 .. +7 (HD >= 128, piece r) or 4c16 .. +3 (HD == 64): 16 lanes
+//    cover one row, coalesced.
+template <int HD>
+struct KVTile {
+    static constexpr int KS = HD / 32;
+    static constexpr int VR = HD >= 128 ? HD / 128 : 1;
+    static constexpr int VW = HD >= 128 ? 8 : 4;  // halfs per V piece
+    f16x8 k[KS];
+    RawF16<VW> v[4][VR];
+};
 
-    int lo, hi, cur_begin;
+template <int HD>
+__device__ __forceinline__ int v_dim(int c16, int r, int j) {
+    return HD >= 128 ? 128 * r + 8 * c16 + j : 4 * c16 + j;
+}
+
+// Streaming loads: the cache is read once per call.
+__device__ __forceinline__ f16x8 ld_stream8(const f16* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+}
+__device__ __forceinline__ f16x4 ld_stream4(const f16* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
+}
+
+// Merge workgroup blockIdx.x: thread (hl, part, col) folds partials part,
+// part + m_parts, ... (at most kMergePer) of float4 column col of item
+// blockIdx.x * m_heads + hl, where an item is (query row, head, slice of
+// 4 * m_cols dims).  Items whose row had a single split were written by the
+// split kernel and are skipped.
+template <int HD, int MODE>
+__global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
+    const int tid = threadIdx.x;
+    const int cols = a.m_cols, parts = a.m_parts;
+    const int hl = tid / (cols * parts);
+    const int part = (tid / cols) % parts, col = tid % cols;
+    const int item = blockIdx.x * a.m_heads + hl;
+    const bool have = hl < a.m_heads && item < a.n_q * a.H * a.m_slices;
+    const int slice = item % a.m_slices;
+    const int rest = item / a.m_slices;
+    const int h = rest % a.H, qi = rest / a.H;
+    int p_u = 0;
+    if (have) {
+        int lo, hi;
+        unit_range<MODE>(a, qi, lo, hi);
+        const int n_tiles = (hi - lo + kTile) / kTile;
+        p_u = (n_tiles + a.tps - 1) / a.tps;
+    }
+    const bool merge = have && p_u > 1;
+    const size_t row = (size_t)qi * a.H + h;
+    const int d0 = 4 * (slice * cols + col);
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (merge) {
+        const float* po = a.part_o + row * a.P * HD + d0;
+        const float* pml = a.part_ml + row * a.P * 2;
+        float m[kMergePer], l[kMergePer];
+        f32x4 x[kMergePer];
+#pragma unroll
+        for (int k = 0; k < kMergePer; ++k) {
+            const int s = part + k * parts;
+            const int sc = s < p_u ? s : 0;  // a valid partial; weighted out below
+            const f32x2 ml = *reinterpret_cast<const f32x2*>(pml + 2 * sc);
+            m[k] = s < p_u ? ml[0] : -INFINITY;
+            l[k] = ml[1];
+            x[k] = *reinterpret_cast<const f32x4*>(po + (size_t)sc * HD);
+        }
+#pragma unroll
+        for (int k = 0; k < kMergePer; ++k) m_run = fmaxf(m_run, m[k]);
+        if (m_run > -INFINITY) {  // else this thread has no partial: exp2(-inf + inf) is NaN
+#pragma unroll
+            for (int k = 0; k < kMergePer; ++k) {
+                const float w = fast_exp2(m[k] - m_run);  // 0 for the unused slots
+                l_run = fmaf(l[k], w, l_run);
+                acc[0] = fmaf(x[k][0], w, acc[0]);
+                acc[1] = fmaf(x[k][1], w, acc[1]);
+                acc[2] = fmaf(x[k][2], w, acc[2]);
+                acc[3] = fmaf(x[k][3], w, acc[3]);
+            }
+        }
+    }
+    // Tree over the parts of each (item, column): tid and tid + stride*cols.
+    __shared__ float s_m[kDecThreads], s_l[kDecThreads];
+    __shared__ f32x4 s_acc[kDecThreads];
+    s_m[tid] = m_run;
+    s_l[tid] = l_run;
+    s_acc[tid] = acc;
+    for (int stride = parts / 2; stride >= 1; stride >>= 1) {
+        __syncthreads();
+        if (part < stride) {
+            const int o = tid + stride * cols;
+            const float m2 = s_m[o];
+            const float mn = fmaxf(m_run, m2);
+            if (mn > -INFINITY) {
+                const float c0 = fast_exp2(m_run - mn), c1 = fast_exp2(m2 - mn);
+                const f32x4 y = s_acc[o];
+                l_run = l_run * c0 + s_l[o] * c1;
+                acc[0] = acc[0] * c0 + y[0] * c1;
+                acc[1] = acc[1] * c0 + y[1] * c1;
+                acc[2] = acc[2] * c0 + y[2] * c1;
+                acc[3] = acc[3] * c0 + y[3] * c1;
+                m_run = mn;
+            }
+            s_m[tid] = m_run;
+            s_l[tid] = l_run;
+            s_acc[tid] = acc;
+        }
+    }
+    if (merge && part == 0) {
+        const float inv = 1.f / l_run;
+        *reinterpret_cast<f32x4*>(a.out + row * HD + d0) =
+            f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    }
+}
+
+template <typename QT, int HD, int GB, int HW, int MODE>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) {
+    using Tile = KVTile<HD>;
+    constexpr int KS = Tile::KS, VR = Tile::VR, VW = Tile::VW;
+    constexpr int DPL = HD / 16;  // V dims per lane
+    constexpr int WPH = kWaves / HW;  // waves per kv head
+    constexpr bool SPLIT_Q = sizeof(QT) == 4;
+    constexpr bool PIPE = HD <= 128;
+    static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
+    static_assert(VR * VW == DPL, "V lane layout");
+    static_assert(kWaves % HW == 0, "waves per head");
+
+    const int bid = blockIdx.x;
+    const int split = bid % a.P;
+    const int yg = (bid / a.P) % a.n_yg;
+    const int qi = bid / (a.P * a.n_yg);
+    const int kvg = yg / a.n_hblk;  // group of HW kv heads
+    const int hb = yg - kvg * a.n_hblk;
+
+    int lo, hi;
+    unit_range<MODE>(a, qi, lo, hi);
+    const int n_tiles = (hi - lo + kTile) / kTile;
+    const int t_begin = split * a.tps;
+    if (t_begin >= n_tiles) return;  // uniform: this unit needs fewer splits
+    const int t_end = min(t_begin + a.tps, n_tiles);
+    const int p_u = (n_tiles + a.tps - 1) / a.tps;  // splits this unit uses
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int hs = wave % HW, wih = wave / HW;  // head slot, wave within head
+    const int kvh = kvg * HW + hs;
+    const int h0 = kvh * a.G + hb * GB;  // first query head of this wave
+    const int g4 = lane >> 4, c16 = lane & 15;
+
     const f16 *kc, *vc;
-    if constexpr (BATCHED) {
-        // Out-of-range lengths are clamped so every read stays in the cache
-        // the caller sized for max_ctx.
-        const int pos = min(max(a.ctx_lens[qi], 1), a.max_ctx) - 1;
-        lo = (a.window && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-        hi = pos;
+    int cur_begin = INT_MAX;
+    if constexpr (MODE == kModeBatched) {
         kc = a.k_ptrs[qi];
         vc = a.v_ptrs[qi];
-        cur_begin = INT_MAX;
     } else {
-        // attn.wgsl:52-66 (first_visible / last_visible)
-        const int pos = a.base_pos + qi;
-        lo = (a.window && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-        if (a.bidi) {
-            const int end = a.base_pos + a.n_tokens - 1;
-            hi = a.window ? min(end, pos + a.window - 1) : end;
-        } else {
-            hi = pos;
-        }
         kc = a.k;
         vc = a.v;
-        cur_begin = a.k_cur ? a.base_pos : INT_MAX;
+        if (MODE == kModeGeneral && a.k_cur) cur_begin = a.base_pos;
     }
-    const int n_chunks = (hi - lo + 1 + CH - 1) / CH;
-    if (wg >= n_chunks) return;  // uniform: more workgroups than chunks
-    const int P = a.P;
-    const int p_eff = min(P, n_chunks);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g4 = lane >> 4, c16 = lane & 15;
-    const int w = a.window;
-
-    // Q^T as the MFMA B operand: column c16, dims KD*g4 + 8*s + j.
-    f16x8 qf[KSTEP];
-    {
-        int head = -1;
-        bool lo_part = false;
-        if (c16 < GB) {
-            head = h0 + c16;
-        } else if (SPLIT_Q && c16 < 2 * GB) {
-            head = h0 + c16 - GB;
-            lo_part = true;
+    // Key position -> row pointer (no branches: selects only).
+    auto row_ptr = [&](const f16* cache, const f16* cur, int p) -> const f16* {
+        if constexpr (MODE == kModeLinear) {
+            return cache + (size_t)p * a.kv_dim + kvh * HD;
+        } else {
+            int s = p;
+            if (a.window) {
+                const uint32_t qd = (uint32_t)(((uint64_t)(uint32_t)p * a.w_magic) >> a.w_shift);
+                s = p - (int)qd * a.window;
+            }
+            const f16* rc = cache + (size_t)s * a.kv_dim;
+            const f16* ru = cur + (size_t)(p - a.base_pos) * a.kv_dim;
+            return (p >= cur_begin ? ru : rc) + kvh * HD;
         }
+    };
+
+    // Issue the loads of tile `t` (keys lo + 16t ..); rows past hi are
+    // clamped to hi (their scores are masked).
+    auto load_tile = [&](int t, Tile& b) {
+        const int kt = lo + kTile * t;
+        const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
 #pragma unroll
-        for (int s = 0; s < KSTEP; ++s) {
-            f16x8 v = {};
-            if (head >= 0) {
-                const size_t qo = ((size_t)qi * a.H + head) * HD + KD * g4 + 8 * s;
-                if constexpr (SPLIT_Q) {
-                    const float* qp = reinterpret_cast<const float*>(a.q) + qo;
-                    const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
-                    const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
-                    const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8(krow + 32 * s + 8 * g4);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const f16 hi16 = (f16)xs[j];
-                        v[j] = lo_part ? (f16)(xs[j] - (float)hi16) : hi16;
-                    }
+        for (int i = 0; i < 4; ++i) {
+            const f16* vrow = row_ptr(vc, a.v_cur, min(kt + 4 * g4 + i, hi));
+#pragma unroll
+            for (int r = 0; r < VR; ++r) {
+                const f16* vp = vrow + v_dim<HD>(c16, r, 0);
+                if constexpr (VW == 8) {
+                    const f16x8 x = ld_stream8(vp);
+                    b.v[i][r].v[0] = f16x4{x[0], x[1], x[2], x[3]};
+                    b.v[i][r].v[1] = f16x4{x[4], x[5], x[6], x[7]};
                 } else {
-                    v = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qo);
+                    b.v[i][r].v[0] = ld_stream4(vp);
                 }
+            }
+        }
+    };
+
+    // This wave's tiles: t_begin + wih, + WPH, ... below t_end.
+    const int my_n = t_begin + wih < t_end ? (t_end - t_begin - wih + WPH - 1) / WPH : 0;
+    auto tile_of = [&](int j) { return t_begin + wih + j * WPH; };
+
+    __shared__ __attribute__((aligned(16))) float sm_o[kWaves][GB][HD];
+    __shared__ float sm_m[kWaves][GB];
+    __shared__ float sm_l[kWaves][GB];
+    // Per-wave LDS slots: p[key][head] and corr[group][head] of the tile.
+    __shared__ __attribute__((aligned(16))) float P_s[kWaves][kTile][8];
+    __shared__ __attribute__((aligned(16))) float C_s[kWaves][4][8];
+
+    // Everything from the first load to the wave's partial sits in one
+    // uniform branch: no path merges loads issued with loads not issued, so
+    // the compiler's wait counts stay exact.
+    if (my_n > 0) {
+        // Q^T as the MFMA B operand: column c16, dims 32s + 8g4 + j.  Columns
+        // past the query heads read a valid row and are zeroed (no branches).
+        // The raw loads go out first, the tile prefetch next, and the f16
+        // conversion waits only for the Q loads.
+        const bool hi_col = c16 < GB;
+        const bool lo_col = SPLIT_Q && !hi_col && c16 < 2 * GB;
+        const int qhead = h0 + (hi_col ? c16 : (lo_col ? c16 - GB : 0));
+        using QRaw = typename std::conditional<SPLIT_Q, f32x4, f16x8>::type;
+        constexpr int QN = SPLIT_Q ? 2 : 1;
+        QRaw qraw[KS][QN];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const size_t qo = ((size_t)qi * a.H + qhead) * HD + 32 * s + 8 * g4;
+            if constexpr (SPLIT_Q) {
+                const float* qp = reinterpret_cast<const float*>(a.q) + qo;
+                qraw[s][0] = *reinterpret_cast<const f32x4*>(qp);
+                qraw[s][QN - 1] = *reinterpret_cast<const f32x4*>(qp + 4);
+            } else {
+                qraw[s][0] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qo);
+            }
+        }
+        // The two prefetches are unconditional (a wave with one tile reads it
+        // twice), so every path into the loop has the same loads in flight and
+        // the compiler's wait counts stay exact.
+        Tile b0, b1;
+        const int last_t = my_n - 1;
+        if constexpr (PIPE) {
+            load_tile(tile_of(0), b0);
+            load_tile(tile_of(min(1, last_t)), b1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        f16x8 qf[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            f16x8 v;
+            if constexpr (SPLIT_Q) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = qraw[s][j / 4][j % 4];
+                    const f16 hi16 = (f16)x;
+                    const f16 lo16 = (f16)(x - (float)hi16);
+                    v[j] = hi_col ? hi16 : (lo_col ? lo16 : (f16)0.f);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = hi_col ? qraw[s][0][j] : (f16)0.f;
             }
             qf[s] = v;
         }
-    }
 
-    // Softmax state of column c16 (meaningful for c16 < GB).
-    float m_run = -1e30f, l_run = 0.f;
-    float o[GB][DPL];
+        // Online-softmax state.  Each 16-lane group g4 runs its own stream over
+        // keys 4g4..4g4+3 of every tile: lane (c16 < GB, g4) holds the running
+        // max and sum of head c16, lane (g4, c16) the group's o over its dims.
+        float m_run = -1e30f, l_run = 0.f;
+        float o[GB][DPL];
 #pragma unroll
-    for (int h = 0; h < GB; ++h)
+        for (int h = 0; h < GB; ++h)
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
+            for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
 
-    // Per-wave LDS slots: p[tile][key][head] and corr[tile][head].
-    __shared__ float P_s[kWaves][kTU][16][8];
-    __shared__ float C_s[kWaves][kTU][8];
-
-    // This wave's work: group j is chunk wg + j*P, of which the wave takes
-    // the kTU tiles starting at key wave*16*kTU.  Groups are double-buffered
-    // in registers: group j+1 is loaded while group j is computed.
-    struct Tiles {
-        f16x8 k[kTU][KSTEP];
-        RawF16<DPL> v[kTU][4];
-    };
-    auto row_of = [&](const f16* cache, const f16* cur, int p, int k0, int s_base) -> const f16* {
-        if (p >= cur_begin) return cur + (size_t)(p - a.base_pos) * a.kv_dim + kvh * HD;
-        int s = p;
-        if (w) {
-            s = s_base + (p - k0);
-            if (s >= w) s -= w;
-            if (s >= w) s %= w;
-        }
-        return cache + (size_t)s * a.kv_dim + kvh * HD;
-    };
-    auto load_group = [&](int j, Tiles& b) {
-        const int k0 = lo + (wg + j * P) * CH;
-        const int k1 = min(k0 + CH, hi + 1);
-        const int tb = k0 + wave * 16 * kTU;
-        if (tb >= k1) return;
-        const int s_base = w ? k0 % w : 0;
-#pragma unroll
-        for (int t = 0; t < kTU; ++t) {
-            const int base_t = tb + 16 * t;
-            const int pk = min(base_t + c16, k1 - 1);
-            const f16* krow = row_of(kc, a.k_cur, pk, k0, s_base) + KD * g4;
-#pragma unroll
-            for (int s = 0; s < KSTEP; ++s) b.k[t][s] = *reinterpret_cast<const f16x8*>(krow + 8 * s);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int pv = min(base_t + 4 * i + g4, k1 - 1);
-                load_raw<DPL>(row_of(vc, a.v_cur, pv, k0, s_base) + DPL * c16, b.v[t][i]);
-            }
-        }
-    };
-    auto compute_group = [&](int j, const Tiles& b) {
-        const int k0 = lo + (wg + j * P) * CH;
-        const int k1 = min(k0 + CH, hi + 1);
-        const int tb = k0 + wave * 16 * kTU;
-        if (tb >= k1) return;
-        wave_lds_sync();  // the previous group's P.V reads are done
-#pragma unroll
-        for (int t = 0; t < kTU; ++t) {
-            const int base_t = tb + 16 * t;
+        const int key_end = hi + 1;
+        auto compute_tile = [&](int t, const Tile& b) {
+            const int kt = lo + kTile * t;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < KSTEP; ++s)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[t][s], qf[s], acc, 0, 0, 0);
+            for (int s = 0; s < KS; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], qf[s], acc, 0, 0, 0);
             float x[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float sv = acc[i];
                 if constexpr (SPLIT_Q) sv += row_rotate_down<GB>(sv);
-                const int key = base_t + 4 * g4 + i;
-                x[i] = key < k1 ? sv * a.c : -INFINITY;
+                x[i] = kt + 4 * g4 + i < key_end ? sv * a.c : -INFINITY;
             }
-            float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            tm = fmaxf(tm, shfl_xor(tm, 16));
-            tm = fmaxf(tm, shfl_xor(tm, 32));
+            const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
             const float mn = fmaxf(m_run, tm);
             const float corr = fast_exp2(m_run - mn);
             m_run = mn;
-            float ps = 0.f;
+            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = fast_exp2(x[i] - mn);
-                ps += p;
-                if (c16 < GB) P_s[wave][t][4 * g4 + i][c16] = p;
+            for (int i = 0; i < 4; ++i) p[i] = fast_exp2(x[i] - mn);
+            l_run = l_run * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+            if (c16 < GB) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) P_s[wave][4 * g4 + i][c16] = p[i];
+                C_s[wave][g4][c16] = corr;
             }
-            l_run = l_run * corr + ps;
-            if (c16 < GB && g4 == 0) C_s[wave][t][c16] = corr;
-        }
-        wave_lds_sync();
+            wave_lds_sync();
+            float cr[GB];
 #pragma unroll
-        for (int t = 0; t < kTU; ++t) {
-            float corr[GB];
-#pragma unroll
-            for (int h = 0; h < GB; ++h) corr[h] = C_s[wave][t][h];
+            for (int h = 0; h < GB; ++h) cr[h] = C_s[wave][g4][h];
 #pragma unroll
             for (int h = 0; h < GB; ++h)
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) o[h][d] *= corr[h];
+                for (int d = 0; d < DPL; ++d) o[h][d] *= cr[h];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int kk = 4 * i + g4;
+                float pv[GB];
 #pragma unroll
-                for (int h = 0; h < GB; ++h) {
-                    const float p = P_s[wave][t][kk][h];
+                for (int h = 0; h < GB; ++h) pv[h] = P_s[wave][4 * g4 + i][h];
 #pragma unroll
-                    for (int d = 0; d < DPL; ++d) o[h][d] = fmaf(p, raw_at<DPL>(b.v[t][i], d), o[h][d]);
-                }
+                for (int r = 0; r < VR; ++r)
+#pragma unroll
+                    for (int j = 0; j < VW; ++j) {
+                        const float vv = raw_at<VW>(b.v[i][r], j);
+#pragma unroll
+                        for (int h = 0; h < GB; ++h) o[h][VW * r + j] = fmaf(pv[h], vv, o[h][VW * r + j]);
+                    }
             }
-        }
-    };
+            wave_lds_sync();  // this tile's P/corr reads are done before the next writes
+            // Keep the P.V arithmetic here: without this the compiler sinks it
+            // past the next prefetch, which then has to wait for every load.
+#pragma unroll
+            for (int h = 0; h < GB; ++h)
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) asm volatile("" : "+v"(o[h][d]));
+            asm volatile("" : "+v"(m_run), "+v"(l_run));
+        };
 
-    const int n_groups = (n_chunks - wg + P - 1) / P;  // chunks wg, wg+P, ... below n_chunks
-    if constexpr (PIPE) {
-        Tiles buf0, buf1;
-        load_group(0, buf0);
-        for (int j = 0; j < n_groups; j += 2) {
-            if (j + 1 < n_groups) load_group(j + 1, buf1);
-            compute_group(j, buf0);
-            if (j + 1 >= n_groups) break;
-            if (j + 2 < n_groups) load_group(j + 2, buf0);
-            compute_group(j + 1, buf1);
-        }
-    } else {
-        Tiles buf;
-        for (int j = 0; j < n_groups; ++j) {
-            load_group(j, buf);
-            compute_group(j, buf);
-        }
-    }
-
-    // Reduce the wave: l over the four lanes of each column, o over the four
-    // key groups (all share the column's running max).
-    l_run += shfl_xor(l_run, 16);
-    l_run += shfl_xor(l_run, 32);
-#pragma unroll
-    for (int h = 0; h < GB; ++h)
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) {
-            float x = o[h][d];
-            x += shfl_xor(x, 16);
-            x += shfl_xor(x, 32);
-            o[h][d] = x;
-        }
-
-    __shared__ float sm_o[kWaves][GB][HD];
-    __shared__ float sm_m[kWaves][GB];
-    __shared__ float sm_l[kWaves][GB];
-    if (g4 == 0) {
-#pragma unroll
-        for (int h = 0; h < GB; ++h)
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) sm_o[wave][h][DPL * c16 + d] = o[h][d];
-        if (c16 < GB) {
-            sm_m[wave][c16] = m_run;
-            sm_l[wave][c16] = l_run;
-        }
-    }
-    __syncthreads();
-
-    const size_t qh0 = (size_t)qi * a.H + h0;  // first (query, head) row of this unit
-    for (int idx = tid; idx < GB * HD; idx += kDecThreads) {
-        const int g = idx / HD, d = idx - g * HD;
-        float M = sm_m[0][g];
-#pragma unroll
-        for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, sm_m[ww][g]);
-        float O = 0.f, L = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) {
-            const float sc = fast_exp2(sm_m[ww][g] - M);
-            O = fmaf(sm_o[ww][g][d], sc, O);
-            L = fmaf(sm_l[ww][g], sc, L);
-        }
-        if (p_eff == 1) {
-            a.out[(qh0 + g) * HD + d] = O / L;
+        if constexpr (PIPE) {
+            // Pairs of tiles while two more remain (the loop body has one
+            // shape, no early exit, so its wait counts are exact), then the
+            // last one to three tiles on straight-line paths that load
+            // nothing past the wave's end.
+            int j = 0;
+            for (; j + 3 < my_n; j += 2) {
+                compute_tile(tile_of(j), b0);
+                __builtin_amdgcn_sched_barrier(0);
+                load_tile(tile_of(j + 2), b0);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_tile(tile_of(j + 1), b1);
+                __builtin_amdgcn_sched_barrier(0);
+                load_tile(tile_of(j + 3), b1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const int rest = my_n - j;
+            if (rest == 3) {
+                compute_tile(tile_of(j), b0);
+                __builtin_amdgcn_sched_barrier(0);
+                load_tile(tile_of(j + 2), b0);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_tile(tile_of(j + 1), b1);
+                compute_tile(tile_of(j + 2), b0);
+            } else if (rest == 2) {
+                compute_tile(tile_of(j), b0);
+                compute_tile(tile_of(j + 1), b1);
+            } else {
+                compute_tile(tile_of(j), b0);
+            }
         } else {
-            const size_t pidx = (qh0 + g) * P + wg;
-            st_co(a.part_o + pidx * HD + d, O);
-            if (d == 0) {
-                st_co(a.part_ml + pidx * 2, M);
-                st_co(a.part_ml + pidx * 2 + 1, L);
+            for (int j = 0; j < my_n; ++j) {
+                load_tile(tile_of(j), b0);
+                compute_tile(tile_of(j), b0);
             }
         }
-    }
-    if (p_eff == 1) return;
 
-    // Count this workgroup in once its sc1 stores are acknowledged; the last
-    // one merges the unit's partials and resets the unit's counter.
-    __shared__ int s_last;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(a.ctr_arrive + unit, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = old == (uint32_t)p_eff - 1;
-        if (last) __hip_atomic_store(a.ctr_arrive + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
+        // Combine the wave's four group streams: M = max of the group maxima;
+        // group g is weighted by exp2(m_g - M), in l and in o.
+        float M = fmaxf(m_run, shfl_xor(m_run, 16));
+        M = fmaxf(M, shfl_xor(M, 32));
+        const float gsc = fast_exp2(m_run - M);
+        float L = l_run * gsc;
+        L += shfl_xor(L, 16);
+        L += shfl_xor(L, 32);
+        if (c16 < GB) C_s[wave][g4][c16] = gsc;
+        wave_lds_sync();
+#pragma unroll
+        for (int h = 0; h < GB; ++h) {
+            const float sc = C_s[wave][g4][h];
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                float x = o[h][d] * sc;
+                x += shfl_xor(x, 16);
+                x += shfl_xor(x, 32);
+                o[h][d] = x;
+            }
+        }
+        if (g4 == 0) {
+#pragma unroll
+            for (int h = 0; h < GB; ++h)
+#pragma unroll
+                for (int r = 0; r < VR; ++r)
+#pragma unroll
+                    for (int j = 0; j < VW; ++j) sm_o[wave][h][v_dim<HD>(c16, r, j)] = o[h][VW * r + j];
+            if (c16 < GB) {
+                sm_m[wave][c16] = M;
+                sm_l[wave][c16] = L;
+            }
+        }
+    } else if (c16 < GB && g4 == 0) {
+        // A wave without tiles contributes nothing: weight exp2(-1e30 - M) = 0.
+        sm_m[wave][c16] = -1e30f;
+        sm_l[wave][c16] = 0.f;
+        for (int d = 0; d < HD; ++d) sm_o[wave][c16][d] = 0.f;
     }
     __syncthreads();
-    if (!s_last) return;
 
-    // Merge: wave g < GB computes head g's weights over the partials
-    // (lane s); then thread (part, column) sums every SP-th partial of one
-    // float4 column and the parts are added in LDS.
-    __shared__ float s_w[GB][kMaxP];
-    __shared__ float s_L[GB];
-    if (wave < GB) {
-        const int g = wave;
-        const float* ml = a.part_ml + (qh0 + g) * P * 2;
-        float m = -1e30f, l = 0.f;
-        if (lane < p_eff) {
-            m = ld_co(ml + lane * 2);
-            l = ld_co(ml + lane * 2 + 1);
-        }
-        float M = m;
+    // Combine the WPH waves of each head slot: element (hs, g, d) of the
+    // workgroup; waves hs, hs + HW, ... hold its parts.
+    for (int idx = tid; idx < HW * GB * HD; idx += kDecThreads) {
+        const int e_hs = idx / (GB * HD);
+        const int rem = idx - e_hs * (GB * HD);
+        const int g = rem / HD, d = rem - g * HD;
+        float Mw = sm_m[e_hs][g];
 #pragma unroll
-        for (int x = 1; x < 64; x <<= 1) M = fmaxf(M, shfl_xor(M, x));
-        const float wgt = lane < p_eff ? fast_exp2(m - M) : 0.f;
-        float L = wgt * l;
+        for (int ww = 1; ww < WPH; ++ww) Mw = fmaxf(Mw, sm_m[e_hs + ww * HW][g]);
+        float O = 0.f, Lw = 0.f;
 #pragma unroll
-        for (int x = 1; x < 64; x <<= 1) L += shfl_xor(L, x);
-        s_w[g][lane] = wgt;
-        if (lane == 0) s_L[g] = L;
-    }
-    __syncthreads();
-    constexpr int NCOL = GB * HD / 4;
-    constexpr int SP = kDecThreads / NCOL >= 1 ? kDecThreads / NCOL : 1;
-    __shared__ f32x4 s_red[SP][NCOL];
-    for (int idx = tid; idx < SP * NCOL; idx += kDecThreads) {
-        const int part = idx / NCOL, col = idx % NCOL;
-        const int g = col / (HD / 4), d4 = col % (HD / 4);
-        const float* src = a.part_o + (qh0 + g) * P * HD + 4 * d4;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = part; s < p_eff; s += SP) {
-            const float wgt = s_w[g][s];
-            const float* p = src + (size_t)s * HD;
-            acc[0] = fmaf(wgt, ld_co(p), acc[0]);
-            acc[1] = fmaf(wgt, ld_co(p + 1), acc[1]);
-            acc[2] = fmaf(wgt, ld_co(p + 2), acc[2]);
-            acc[3] = fmaf(wgt, ld_co(p + 3), acc[3]);
+        for (int ww = 0; ww < WPH; ++ww) {
+            const int w = e_hs + ww * HW;
+            const float sc = fast_exp2(sm_m[w][g] - Mw);
+            O = fmaf(sm_o[w][g][d], sc, O);
+            Lw = fmaf(sm_l[w][g], sc, Lw);
         }
-        s_red[part][col] = acc;
-    }
-    __syncthreads();
-    for (int col = tid; col < NCOL; col += kDecThreads) {
-        const int g = col / (HD / 4), d4 = col % (HD / 4);
-        f32x4 acc = s_red[0][col];
-#pragma unroll
-        for (int part = 1; part < SP; ++part) {
-            const f32x4 x = s_red[part][col];
-            acc[0] += x[0];
-            acc[1] += x[1];
-            acc[2] += x[2];
-            acc[3] += x[3];
+        const int head = (kvg * HW + e_hs) * a.G + hb * GB + g;
+        const size_t row = (size_t)qi * a.H + head;
+        if (p_u == 1) {
+            a.out[row * HD + d] = O / Lw;
+        } else {
+            const size_t pidx = row * a.P + split;
+            a.part_o[pidx * HD + d] = O;
+            if (d == 0) {
+                a.part_ml[pidx * 2] = Mw;
+                a.part_ml[pidx * 2 + 1] = Lw;
+            }
         }
-        const float inv = 1.f / s_L[g];
-        *reinterpret_cast<f32x4*>(a.out + (qh0 + g) * HD + 4 * d4) =
-            f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
     }
 }
 
 // ------------------------------------------------------------------ host --
 
 struct DecodePlan {
-    int P, n_hblk, gb;
-    size_t ctr_bytes, ml_bytes, o_bytes;
-    size_t total() const { return ctr_bytes + ml_bytes + o_bytes; }
+    int P, tps, n_hblk, gb, hw;
+    int n_main, n_yg;
+    int n_merge, m_cols, m_parts, m_heads, m_slices;
+    size_t ml_bytes, o_bytes;
+    size_t total() const { return ml_bytes + o_bytes; }
 };
 
-// Query heads per workgroup: the largest divisor of G within the register
-// budget (o holds gb * hd/16 floats per lane) and the 16 MFMA columns (an
-// fp32 query takes two columns per head).
+// Query heads per wave: the largest divisor of G within the register budget
+// (o holds gb * hd/16 floats per lane, K/V tiles grow with hd) and the 16
+// MFMA columns (an fp32 query takes two columns per head).
 static int pick_gb(int G, int hd) {
-    const int cap = hd >= 512 ? 1 : (hd == 256 ? 4 : 8);
+    const int cap = hd >= 512 ? 1 : (hd == 256 ? 2 : (hd == 128 ? 6 : 8));
     for (int gb = cap; gb >= 1; --gb)
         if (G % gb == 0) return gb;
     return 1;
 }
 
+// kv heads per workgroup: the largest power of two <= kWaves dividing Hkv.
+static int pick_hw(int Hkv) {
+    for (int hw = kWaves; hw > 1; hw >>= 1)
+        if (Hkv % hw == 0) return hw;
+    return 1;
+}
+
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Workgroups the heuristic aims for: one 8-wave workgroup per CU on 256 CUs.
-// LMX_DECODE_TARGET_WGS overrides it for tuning sweeps.
+static long env_long(const char* name, long dflt) {
+    const char* e = std::getenv(name);
+    const long x = e ? std::atol(e) : 0;
+    return x > 0 ? x : dflt;
+}
+
+// Workgroups the heuristic aims for (one 8-wave workgroup per CU on 256 CUs)
+// and the fewest tiles a wave should get before a unit is split further.
+// LMX_DECODE_TARGET_WGS / LMX_DECODE_MIN_TILES override them for tuning sweeps.
 static long target_wgs() {
-    static long v = [] {
-        const char* e = std::getenv("LMX_DECODE_TARGET_WGS");
-        long x = e ? std::atol(e) : 0;
-        return x > 0 ? x : 256L;
-    }();
+    static long v = env_long("LMX_DECODE_TARGET_WGS", 256);
+    return v;
+}
+static long min_tiles_per_wave() {
+    static long v = env_long("LMX_DECODE_MIN_TILES", 2);
     return v;
 }
 
@@ -474,37 +610,80 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
     const int G = H / Hkv;
     pl.gb = pick_gb(G, hd);
     pl.n_hblk = G / pl.gb;
-    const long units = (long)n_q * Hkv * pl.n_hblk;
-    const long n_chunks = (max_vis + chunk_keys(hd, pl.gb) - 1) / chunk_keys(hd, pl.gb);
+    pl.hw = pick_hw(Hkv);
+    pl.n_yg = (Hkv / pl.hw) * pl.n_hblk;
+    const long units = (long)n_q * pl.n_yg;
+    const long n_tiles = (max_vis + kTile - 1) / kTile;
+    const long wph = kWaves / pl.hw;
     long P = (target_wgs() + units - 1) / units;
-    if (P > n_chunks) P = n_chunks;
+    const long cap = n_tiles / (wph * min_tiles_per_wave());
+    if (P > cap) P = cap;
     if (P > kMaxP) P = kMaxP;
     if (P < 1) P = 1;
+    const long tps = (n_tiles + P - 1) / P;
+    P = (n_tiles + tps - 1) / tps;  // drop splits that would be empty
     pl.P = (int)P;
+    pl.tps = (int)tps;
+    pl.n_main = (int)(P * units);
     if (P > 1) {
-        pl.ctr_bytes = round_up((size_t)units * 4, 256);
+        // Merge layout: parts (a power of two) so that each thread folds at
+        // most kMergePer partials, float4 columns per item, items per
+        // workgroup to fill its kDecThreads threads.
+        int parts = 1;
+        while (parts * kMergePer < P) parts <<= 1;
+        int cols = hd / 4;
+        while (cols * parts > kDecThreads) cols >>= 1;
+        pl.m_parts = parts;
+        pl.m_cols = cols;
+        pl.m_heads = kDecThreads / (cols * parts);
+        pl.m_slices = (hd / 4) / cols;
+        const long items = (long)n_q * H * pl.m_slices;
+        pl.n_merge = (int)((items + pl.m_heads - 1) / pl.m_heads);
         pl.ml_bytes = round_up((size_t)n_q * H * P * 2 * 4, 256);
         pl.o_bytes = round_up((size_t)n_q * H * P * hd * 4, 256);
     }
     return pl;
 }
 
-template <typename QT, bool BATCHED>
-static lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, dim3 grid, hipStream_t st) {
-#define LMX_DEC_CASE(HDV, GBV)                                                                   \
-    if (hd == HDV && gb == GBV) {                                                                \
-        hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, BATCHED>), grid, dim3(kDecThreads), \
-                           0, st, a);                                                            \
-        return LMX_OK;                                                                           \
+template <typename QT, int MODE, int HW>
+static lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, dim3 grid, hipStream_t st) {
+#define LMX_DEC_CASE(HDV, GBV)                                                                     \
+    if (hd == HDV && gb == GBV) {                                                                  \
+        hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE>), grid, dim3(kDecThreads), \
+                           0, st, a);                                                              \
+        return LMX_OK;                                                                             \
     }
     LMX_DEC_CASE(64, 1) LMX_DEC_CASE(64, 2) LMX_DEC_CASE(64, 3) LMX_DEC_CASE(64, 4)
     LMX_DEC_CASE(64, 5) LMX_DEC_CASE(64, 6) LMX_DEC_CASE(64, 7) LMX_DEC_CASE(64, 8)
     LMX_DEC_CASE(128, 1) LMX_DEC_CASE(128, 2) LMX_DEC_CASE(128, 3) LMX_DEC_CASE(128, 4)
-    LMX_DEC_CASE(128, 5) LMX_DEC_CASE(128, 6) LMX_DEC_CASE(128, 7) LMX_DEC_CASE(128, 8)
-    LMX_DEC_CASE(256, 1) LMX_DEC_CASE(256, 2) LMX_DEC_CASE(256, 3) LMX_DEC_CASE(256, 4)
+    LMX_DEC_CASE(128, 5) LMX_DEC_CASE(128, 6)
+    LMX_DEC_CASE(256, 1) LMX_DEC_CASE(256, 2)
     LMX_DEC_CASE(512, 1)
 #undef LMX_DEC_CASE
     return LMX_E_UNSUPPORTED;
+}
+
+template <typename QT, int MODE>
+static lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, int hw, dim3 grid,
+                                hipStream_t st) {
+    switch (hw) {
+        case 8: return launch_decode_hw<QT, MODE, 8>(a, hd, gb, grid, st);
+        case 4: return launch_decode_hw<QT, MODE, 4>(a, hd, gb, grid, st);
+        case 2: return launch_decode_hw<QT, MODE, 2>(a, hd, gb, grid, st);
+        default: return launch_decode_hw<QT, MODE, 1>(a, hd, gb, grid, st);
+    }
+}
+
+template <int MODE>
+static lmx_status launch_merge(const DecodeArgs& a, int hd, dim3 grid, hipStream_t st) {
+    switch (hd) {
+        case 64: hipLaunchKernelGGL((attn_merge_kernel<64, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
+        case 128: hipLaunchKernelGGL((attn_merge_kernel<128, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
+        case 256: hipLaunchKernelGGL((attn_merge_kernel<256, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
+        case 512: hipLaunchKernelGGL((attn_merge_kernel<512, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
+        default: return LMX_E_UNSUPPORTED;
+    }
+    return LMX_OK;
 }
 
 // Longest visible range over the batch's queries (attn.wgsl:52-66 maximized
@@ -539,30 +718,63 @@ size_t decode_batched_workspace_bytes(const lmx_attn_params* p, int n_seq, int m
     return pl.total();
 }
 
+// Multiply-high constants for p % window over 31-bit p (Granlund-Montgomery:
+// m = floor(2^(31+l) / w) + 1 with l = ceil(log2 w) makes
+// floor(p / w) == (p * m) >> (31 + l) for every 0 <= p < 2^31).
+static void window_magic(uint32_t w, uint32_t* magic, int* shift) {
+    if (w == 0) {
+        *magic = 0;
+        *shift = 0;
+        return;
+    }
+    int l = 0;
+    while ((1ull << l) < w) ++l;
+    *magic = (uint32_t)((1ull << (31 + l)) / w + 1);
+    *shift = 31 + l;
+}
+
 static lmx_status run(DecodeArgs a, const DecodePlan& pl, int n_q, int hd, lmx_dtype q_dt,
-                      bool batched, void* ws, size_t ws_bytes, hipStream_t st) {
+                      int mode, void* ws, size_t ws_bytes, hipStream_t st) {
     if (pl.total() > 0) {
         if (!ws || ws_bytes < pl.total()) return LMX_E_WORKSPACE;
         if (((uintptr_t)ws & 255) != 0) return LMX_E_ALIGN;
         char* b = static_cast<char*>(ws);
-        a.ctr_arrive = reinterpret_cast<uint32_t*>(b);
-        b += pl.ctr_bytes;
         a.part_ml = reinterpret_cast<float*>(b);
         b += pl.ml_bytes;
         a.part_o = reinterpret_cast<float*>(b);
     }
+    a.n_q = n_q;
     a.P = pl.P;
+    a.tps = pl.tps;
     a.n_hblk = pl.n_hblk;
-    dim3 grid(pl.P, a.Hkv * pl.n_hblk, n_q);
+    a.n_main = pl.n_main;
+    a.n_yg = pl.n_yg;
+    a.n_merge = pl.n_merge;
+    a.m_cols = pl.m_cols;
+    a.m_parts = pl.m_parts;
+    a.m_heads = pl.m_heads;
+    a.m_slices = pl.m_slices;
+    window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
+    const dim3 grid((unsigned)pl.n_main);
     (void)hipGetLastError();
     lmx_status s;
+#define LMX_DEC_MODE(QT)                                                                     \
+    (mode == kModeLinear    ? launch_decode<QT, kModeLinear>(a, hd, pl.gb, pl.hw, grid, st)  \
+     : mode == kModeGeneral ? launch_decode<QT, kModeGeneral>(a, hd, pl.gb, pl.hw, grid, st) \
+                            : launch_decode<QT, kModeBatched>(a, hd, pl.gb, pl.hw, grid, st))
     if (q_dt == LMX_F32)
-        s = batched ? launch_decode<float, true>(a, hd, pl.gb, grid, st)
-                    : launch_decode<float, false>(a, hd, pl.gb, grid, st);
+        s = LMX_DEC_MODE(float);
     else
-        s = batched ? launch_decode<f16, true>(a, hd, pl.gb, grid, st)
-                    : launch_decode<f16, false>(a, hd, pl.gb, grid, st);
+        s = LMX_DEC_MODE(f16);
+#undef LMX_DEC_MODE
     if (s != LMX_OK) return s;
+    if (pl.P > 1) {
+        const dim3 mgrid((unsigned)pl.n_merge);
+        s = mode == kModeLinear    ? launch_merge<kModeLinear>(a, hd, mgrid, st)
+            : mode == kModeGeneral ? launch_merge<kModeGeneral>(a, hd, mgrid, st)
+                                   : launch_merge<kModeBatched>(a, hd, mgrid, st);
+        if (s != LMX_OK) return s;
+    }
     LMX_CHECK_LAUNCH();
     return LMX_OK;
 }
@@ -586,8 +798,14 @@ lmx_status decode_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, c
     a.n_tokens = (int)p->n_tokens;
     a.bidi = (int)p->bidi;
     a.c = p->scale * kLog2e;
-    const DecodePlan pl = plan_decode(a.n_tokens, a.H, a.Hkv, (int)p->head_dim, decode_max_vis(p));
-    return run(a, pl, a.n_tokens, (int)p->head_dim, q_dt, false, ws, ws_bytes, st);
+    const int mv = decode_max_vis(p);
+    const DecodePlan pl = plan_decode(a.n_tokens, a.H, a.Hkv, (int)p->head_dim, mv);
+    // Linear addressing reads row p for every visible p: no k_cur rows and no
+    // ring wrap (every visible position is below the window).
+    const long last = (long)p->base_pos + p->n_tokens - 1;
+    const bool linear = !k_cur && (p->window == 0 || last < (long)p->window);
+    return run(a, pl, a.n_tokens, (int)p->head_dim, q_dt, linear ? kModeLinear : kModeGeneral, ws,
+               ws_bytes, st);
 }
 
 lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, const int32_t* ctx_lens,
@@ -610,7 +828,7 @@ lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, cons
     int mv = max_ctx;
     if (a.window && a.window < mv) mv = a.window;
     const DecodePlan pl = plan_decode(n_seq, a.H, a.Hkv, (int)p->head_dim, mv);
-    return run(a, pl, n_seq, (int)p->head_dim, q_dt, true, ws, ws_bytes, st);
+    return run(a, pl, n_seq, (int)p->head_dim, q_dt, kModeBatched, ws, ws_bytes, st);
 }
 
 }  // namespace lmx

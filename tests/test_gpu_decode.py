@@ -124,3 +124,27 @@ def test_repeat_calls_reuse_workspace():
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
     assert_close(outs[0], c.reference(base_pos=19999))
+
+
+def test_workspace_reuse_with_different_inputs():
+    """Split partials cross workgroups through the workspace: alternating two
+    different inputs on one workspace must give each input's own result
+    (stale partials from the previous call would show up here)."""
+    ws = lmx.Workspace()
+    cases = [AttnCase(s, t=1, H=32, Hkv=8, hd=128, n_pos=9000) for s in (21, 22)]
+    dev_in = [(dev(c.q), dev(c.k16, torch.float16), dev(c.v16, torch.float16)) for c in cases]
+    refs = [c.reference(base_pos=8999) for c in cases]
+    for rep in range(3):
+        for i, (q, kc, vc) in enumerate(dev_in):
+            say(f"workspace reuse rep={rep} case={i}")
+            out = lmx.attention(q, kc, vc, n_heads=32, n_kv_heads=8, head_dim=128, base_pos=8999,
+                                workspace=ws)
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), refs[i], what=f"rep {rep} case {i}")
+
+
+@pytest.mark.parametrize("ctx", [16, 17, 127, 128, 129, 1023, 2047, 2049])
+def test_tile_and_split_edges(ctx):
+    """Context lengths around the 16-key tile and the split boundaries."""
+    c = AttnCase(ctx + 5, t=1, H=32, Hkv=8, hd=128, n_pos=ctx)
+    run_case(c, base=ctx - 1)
