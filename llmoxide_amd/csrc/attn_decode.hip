@@ -1,571 +1,8 @@
-// Split-K attention for few query tokens (decode) on gfx950.
-//
-// Replaces, for n_tokens small, the reference's three passes scores_pass /
-// softmax_pass / weighted_v (attn.wgsl:84-232), which give decode only
-// n_heads workgroups and a serial key loop (attn.wgsl:13-17).
-//
-// Work split.  A workgroup owns HW kv heads (one wave group per head) for a
-// block of GB query heads per kv head, one query row, and split s of the
-// visible keys: the contiguous 16-key tiles [s*tps, (s+1)*tps).  With HW = 8
-// and one wave per head, the workgroup's loads cover whole cache rows (a
-// row holds every kv head), which is the access pattern HBM serves fastest;
-// K/V rows are read once for all GB query heads of a kv head (GQA) and with
-// non-temporal loads (they are streamed, never re-read).  Each wave keeps
-// two tiles of K/V in registers: while it computes one, the next one's loads
-// are in flight.  Row addressing is branch-free: a linear cache reads row p,
-// a ring reads slot p % window (multiply-high division), and rows of the
-// current batch can come from a separate k_cur/v_cur buffer.
-//
-// Per wave and tile:
-//   S^T[16 keys x 16 cols] = K Q^T on v_mfma_f32_16x16x32_f16.  Columns
-//   0..GB-1 hold the f16 high part of each query head, columns GB..2GB-1 the
-//   f16 residual (q - hi) of an fp32 query, so q.k is exact to ~2^-22.
-//   Lane (g, c) then holds keys 4g..4g+3 of column c.  Each 16-lane group g
-//   runs its own online softmax over its four keys of every tile (fp32, exp2
-//   with scale*log2(e) folded in), so no value crosses groups inside the
-//   loop; the four streams are merged once at the end.  p goes through a
-//   per-wave LDS slot to the P.V lanes of the same group; those read V rows
-//   coalesced (16 lanes cover one 256-byte row) and accumulate in fp32.
-//
-// Merge.  With one split per unit the workgroup writes the output.  Else
-// each split workgroup stores one partial (max, sum, o[hd]) per query head
-// and a second, small kernel merges them: each of its threads folds up to
-// eight partials of one float4 column (all loads issued at once), and the
-// parts of a column are combined in an LDS tree.  The launch boundary
-// orders the partial stores before the merge loads; no counters, so the
-// pair can be replayed from a captured graph as is.
-#include <climits>
-#include <cstdlib>
-
-#include "common.hpp"
+// Split-K attention for few query tokens (decode): planning and entry points.
+// The kernels and their design notes are in attn_decode.hpp.
+#include "attn_decode.hpp"
 
 namespace lmx {
-
-enum DecodeMode { kModeLinear = 0, kModeGeneral = 1, kModeBatched = 2 };
-
-struct DecodeArgs {
-    const void* q;
-    const f16* k;
-    const f16* v;
-    const f16* const* k_ptrs;
-    const f16* const* v_ptrs;
-    const f16* k_cur;
-    const f16* v_cur;
-    const int32_t* ctx_lens;
-    float* out;
-    float* part_o;          // [n_q][H][P][HD]  per-split partials
-    float* part_ml;         // [n_q][H][P][2]   (max in log2 units, sum)
-    int H, Hkv, G, kv_dim;
-    int base_pos, window, n_tokens, bidi;
-    int P, tps, n_hblk;
-    int n_q;                // query rows (tokens, or sequences when batched)
-    int n_main, n_yg;       // split workgroups; their (kv group, head block) count
-    int n_merge, m_cols, m_parts, m_heads, m_slices;  // merge workgroup layout
-    int max_ctx;            // batched: context lengths are clamped to [1, max_ctx]
-    uint32_t w_magic;       // p % window == p - window * ((p * w_magic) >> w_shift)
-    int w_shift;
-    float c;                // scale * log2(e)
-};
-
-constexpr int kWaves = 8;
-constexpr int kDecThreads = kWaves * 64;
-constexpr int kMaxP = 512;  // splits per unit
-constexpr int kTile = 16;   // keys per wave tile
-constexpr int kMergePer = 8;            // partials per merge thread
-
-// Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
-// batched: the sequence's last position).
-template <int MODE>
-__device__ __forceinline__ void unit_range(const DecodeArgs& a, int qi, int& lo, int& hi) {
-    int pos;
-    if constexpr (MODE == kModeBatched) {
-        // Out-of-range lengths are clamped so every read stays in the cache
-        // the caller sized for max_ctx.
-        pos = min(max(a.ctx_lens[qi], 1), a.max_ctx) - 1;
-        hi = pos;
-    } else {
-        pos = a.base_pos + qi;
-        if (a.bidi) {
-            const int end = a.base_pos + a.n_tokens - 1;
-            hi = a.window ? min(end, pos + a.window - 1) : end;
-        } else {
-            hi = pos;
-        }
-    }
-    lo = (a.window && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-}
-
-// Order LDS traffic between lanes of one wave (LDS executes a wave's
-// accesses in order; this keeps the compiler from reordering them).
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Row rotate within a 16-lane DPP row: lane i receives lane (i + N) % 16.
-template <int N>
-__device__ __forceinline__ float row_rotate_down(float x) {
-    return dpp<0x120 + (16 - N)>(x);  // row_ror:(16-N)
-}
-
-// Per-lane K/V registers of one 16-key tile.
-//  K (MFMA A operand): lane (key c16, group g4), k-step s holds dims
-//    32s + 8g4 .. +7 of key c16: each load covers 64 contiguous bytes per key.
-//  V (P.V operand): load i, lane (g4, c16) holds key 4g4 + i, dims
-//    128r + 8c16 .. +7 (HD >= 128, piece r) or 4c16 .. +3 (HD == 64): 16 lanes
-//    cover one row, coalesced.
-template <int HD>
-struct KVTile {
-    static constexpr int KS = HD / 32;
-    static constexpr int VR = HD >= 128 ? HD / 128 : 1;
-    static constexpr int VW = HD >= 128 ? 8 : 4;  // halfs per V piece
-    f16x8 k[KS];
-    RawF16<VW> v[4][VR];
-};
-
-template <int HD>
-__device__ __forceinline__ int v_dim(int c16, int r, int j) {
-    return HD >= 128 ? 128 * r + 8 * c16 + j : 4 * c16 + j;
-}
-
-// Streaming loads: the cache is read once per call.
-__device__ __forceinline__ f16x8 ld_stream8(const f16* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
-}
-__device__ __forceinline__ f16x4 ld_stream4(const f16* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
-}
-
-// Merge workgroup blockIdx.x: thread (hl, part, col) folds partials part,
-// part + m_parts, ... (at most kMergePer) of float4 column col of item
-// blockIdx.x * m_heads + hl, where an item is (query row, head, slice of
-// 4 * m_cols dims).  Items whose row had a single split were written by the
-// split kernel and are skipped.
-template <int HD, int MODE>
-__global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
-    const int tid = threadIdx.x;
-    const int cols = a.m_cols, parts = a.m_parts;
-    const int hl = tid / (cols * parts);
-    const int part = (tid / cols) % parts, col = tid % cols;
-    const int item = blockIdx.x * a.m_heads + hl;
-    const bool have = hl < a.m_heads && item < a.n_q * a.H * a.m_slices;
-    const int slice = item % a.m_slices;
-    const int rest = item / a.m_slices;
-    const int h = rest % a.H, qi = rest / a.H;
-    int p_u = 0;
-    if (have) {
-        int lo, hi;
-        unit_range<MODE>(a, qi, lo, hi);
-        const int n_tiles = (hi - lo + kTile) / kTile;
-        p_u = (n_tiles + a.tps - 1) / a.tps;
-    }
-    const bool merge = have && p_u > 1;
-    const size_t row = (size_t)qi * a.H + h;
-    const int d0 = 4 * (slice * cols + col);
-    float m_run = -INFINITY, l_run = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (merge) {
-        const float* po = a.part_o + row * a.P * HD + d0;
-        const float* pml = a.part_ml + row * a.P * 2;
-        float m[kMergePer], l[kMergePer];
-        f32x4 x[kMergePer];
-#pragma unroll
-        for (int k = 0; k < kMergePer; ++k) {
-            const int s = part + k * parts;
-            const int sc = s < p_u ? s : 0;  // a valid partial; weighted out below
-            const f32x2 ml = *reinterpret_cast<const f32x2*>(pml + 2 * sc);
-            m[k] = s < p_u ? ml[0] : -INFINITY;
-            l[k] = ml[1];
-            x[k] = *reinterpret_cast<const f32x4*>(po + (size_t)sc * HD);
-        }
-#pragma unroll
-        for (int k = 0; k < kMergePer; ++k) m_run = fmaxf(m_run, m[k]);
-        if (m_run > -INFINITY) {  // else this thread has no partial: exp2(-inf + inf) is NaN
-#pragma unroll
-            for (int k = 0; k < kMergePer; ++k) {
-                const float w = fast_exp2(m[k] - m_run);  // 0 for the unused slots
-                l_run = fmaf(l[k], w, l_run);
-                acc[0] = fmaf(x[k][0], w, acc[0]);
-                acc[1] = fmaf(x[k][1], w, acc[1]);
-                acc[2] = fmaf(x[k][2], w, acc[2]);
-                acc[3] = fmaf(x[k][3], w, acc[3]);
-            }
-        }
-    }
-    // Tree over the parts of each (item, column): tid and tid + stride*cols.
-    __shared__ float s_m[kDecThreads], s_l[kDecThreads];
-    __shared__ f32x4 s_acc[kDecThreads];
-    s_m[tid] = m_run;
-    s_l[tid] = l_run;
-    s_acc[tid] = acc;
-    for (int stride = parts / 2; stride >= 1; stride >>= 1) {
-        __syncthreads();
-        if (part < stride) {
-            const int o = tid + stride * cols;
-            const float m2 = s_m[o];
-            const float mn = fmaxf(m_run, m2);
-            if (mn > -INFINITY) {
-                const float c0 = fast_exp2(m_run - mn), c1 = fast_exp2(m2 - mn);
-                const f32x4 y = s_acc[o];
-                l_run = l_run * c0 + s_l[o] * c1;
-                acc[0] = acc[0] * c0 + y[0] * c1;
-                acc[1] = acc[1] * c0 + y[1] * c1;
-                acc[2] = acc[2] * c0 + y[2] * c1;
-                acc[3] = acc[3] * c0 + y[3] * c1;
-                m_run = mn;
-            }
-            s_m[tid] = m_run;
-            s_l[tid] = l_run;
-            s_acc[tid] = acc;
-        }
-    }
-    if (merge && part == 0) {
-        const float inv = 1.f / l_run;
-        *reinterpret_cast<f32x4*>(a.out + row * HD + d0) =
-            f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-    }
-}
-
-template <typename QT, int HD, int GB, int HW, int MODE>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) {
-    using Tile = KVTile<HD>;
-    constexpr int KS = Tile::KS, VR = Tile::VR, VW = Tile::VW;
-    constexpr int DPL = HD / 16;  // V dims per lane
-    constexpr int WPH = kWaves / HW;  // waves per kv head
-    constexpr bool SPLIT_Q = sizeof(QT) == 4;
-    constexpr bool PIPE = HD <= 128;
-    static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
-    static_assert(VR * VW == DPL, "V lane layout");
-    static_assert(kWaves % HW == 0, "waves per head");
-
-    const int bid = blockIdx.x;
-    const int split = bid % a.P;
-    const int yg = (bid / a.P) % a.n_yg;
-    const int qi = bid / (a.P * a.n_yg);
-    const int kvg = yg / a.n_hblk;  // group of HW kv heads
-    const int hb = yg - kvg * a.n_hblk;
-
-    int lo, hi;
-    unit_range<MODE>(a, qi, lo, hi);
-    const int n_tiles = (hi - lo + kTile) / kTile;
-    const int t_begin = split * a.tps;
-    if (t_begin >= n_tiles) return;  // uniform: this unit needs fewer splits
-    const int t_end = min(t_begin + a.tps, n_tiles);
-    const int p_u = (n_tiles + a.tps - 1) / a.tps;  // splits this unit uses
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int hs = wave % HW, wih = wave / HW;  // head slot, wave within head
-    const int kvh = kvg * HW + hs;
-    const int h0 = kvh * a.G + hb * GB;  // first query head of this wave
-    const int g4 = lane >> 4, c16 = lane & 15;
-
-    const f16 *kc, *vc;
-    int cur_begin = INT_MAX;
-    if constexpr (MODE == kModeBatched) {
-        kc = a.k_ptrs[qi];
-        vc = a.v_ptrs[qi];
-    } else {
-        kc = a.k;
-        vc = a.v;
-        if (MODE == kModeGeneral && a.k_cur) cur_begin = a.base_pos;
-    }
-
-    // Key position -> row pointer (no branches: selects only).
-    auto row_ptr = [&](const f16* cache, const f16* cur, int p) -> const f16* {
-        if constexpr (MODE == kModeLinear) {
-            return cache + (size_t)p * a.kv_dim + kvh * HD;
-        } else {
-            int s = p;
-            if (a.window) {
-                const uint32_t qd = (uint32_t)(((uint64_t)(uint32_t)p * a.w_magic) >> a.w_shift);
-                s = p - (int)qd * a.window;
-            }
-            const f16* rc = cache + (size_t)s * a.kv_dim;
-            const f16* ru = cur + (size_t)(p - a.base_pos) * a.kv_dim;
-            return (p >= cur_begin ? ru : rc) + kvh * HD;
-        }
-    };
-
-    // Issue the loads of tile `t` (keys lo + 16t ..); rows past hi are
-    // clamped to hi (their scores are masked).
-    auto load_tile = [&](int t, Tile& b) {
-        const int kt = lo + kTile * t;
-        const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
-#pragma unroll
-        for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8(krow + 32 * s + 8 * g4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f16* vrow = row_ptr(vc, a.v_cur, min(kt + 4 * g4 + i, hi));
-#pragma unroll
-            for (int r = 0; r < VR; ++r) {
-                const f16* vp = vrow + v_dim<HD>(c16, r, 0);
-                if constexpr (VW == 8) {
-                    const f16x8 x = ld_stream8(vp);
-                    b.v[i][r].v[0] = f16x4{x[0], x[1], x[2], x[3]};
-                    b.v[i][r].v[1] = f16x4{x[4], x[5], x[6], x[7]};
-                } else {
-                    b.v[i][r].v[0] = ld_stream4(vp);
-                }
-            }
-        }
-    };
-
-    // This wave's tiles: t_begin + wih, + WPH, ... below t_end.
-    const int my_n = t_begin + wih < t_end ? (t_end - t_begin - wih + WPH - 1) / WPH : 0;
-    auto tile_of = [&](int j) { return t_begin + wih + j * WPH; };
-
-    __shared__ __attribute__((aligned(16))) float sm_o[kWaves][GB][HD];
-    __shared__ float sm_m[kWaves][GB];
-    __shared__ float sm_l[kWaves][GB];
-    // Per-wave LDS slots: p[key][head] and corr[group][head] of the tile.
-    __shared__ __attribute__((aligned(16))) float P_s[kWaves][kTile][8];
-    __shared__ __attribute__((aligned(16))) float C_s[kWaves][4][8];
-
-    // Everything from the first load to the wave's partial sits in one
-    // uniform branch: no path merges loads issued with loads not issued, so
-    // the compiler's wait counts stay exact.
-    if (my_n > 0) {
-        // Q^T as the MFMA B operand: column c16, dims 32s + 8g4 + j.  Columns
-        // past the query heads read a valid row and are zeroed (no branches).
-        // The raw loads go out first, the tile prefetch next, and the f16
-        // conversion waits only for the Q loads.
-        const bool hi_col = c16 < GB;
-        const bool lo_col = SPLIT_Q && !hi_col && c16 < 2 * GB;
-        const int qhead = h0 + (hi_col ? c16 : (lo_col ? c16 - GB : 0));
-        using QRaw = typename std::conditional<SPLIT_Q, f32x4, f16x8>::type;
-        constexpr int QN = SPLIT_Q ? 2 : 1;
-        QRaw qraw[KS][QN];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const size_t qo = ((size_t)qi * a.H + qhead) * HD + 32 * s + 8 * g4;
-            if constexpr (SPLIT_Q) {
-                const float* qp = reinterpret_cast<const float*>(a.q) + qo;
-                qraw[s][0] = *reinterpret_cast<const f32x4*>(qp);
-                qraw[s][QN - 1] = *reinterpret_cast<const f32x4*>(qp + 4);
-            } else {
-                qraw[s][0] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qo);
-            }
-        }
-        // The two prefetches are unconditional (a wave with one tile reads it
-        // twice), so every path into the loop has the same loads in flight and
-        // the compiler's wait counts stay exact.
-        Tile b0, b1;
-        const int last_t = my_n - 1;
-        if constexpr (PIPE) {
-            load_tile(tile_of(0), b0);
-            load_tile(tile_of(min(1, last_t)), b1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-
-        f16x8 qf[KS];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            f16x8 v;
-            if constexpr (SPLIT_Q) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float x = qraw[s][j / 4][j % 4];
-                    const f16 hi16 = (f16)x;
-                    const f16 lo16 = (f16)(x - (float)hi16);
-                    v[j] = hi_col ? hi16 : (lo_col ? lo16 : (f16)0.f);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = hi_col ? qraw[s][0][j] : (f16)0.f;
-            }
-            qf[s] = v;
-        }
-
-        // Online-softmax state.  Each 16-lane group g4 runs its own stream over
-        // keys 4g4..4g4+3 of every tile: lane (c16 < GB, g4) holds the running
-        // max and sum of head c16, lane (g4, c16) the group's o over its dims.
-        float m_run = -1e30f, l_run = 0.f;
-        float o[GB][DPL];
-#pragma unroll
-        for (int h = 0; h < GB; ++h)
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
-
-        const int key_end = hi + 1;
-        auto compute_tile = [&](int t, const Tile& b) {
-            const int kt = lo + kTile * t;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], qf[s], acc, 0, 0, 0);
-            float x[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float sv = acc[i];
-                if constexpr (SPLIT_Q) sv += row_rotate_down<GB>(sv);
-                x[i] = kt + 4 * g4 + i < key_end ? sv * a.c : -INFINITY;
-            }
-            const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            const float mn = fmaxf(m_run, tm);
-            const float corr = fast_exp2(m_run - mn);
-            m_run = mn;
-            float p[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = fast_exp2(x[i] - mn);
-            l_run = l_run * corr + ((p[0] + p[1]) + (p[2] + p[3]));
-            if (c16 < GB) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) P_s[wave][4 * g4 + i][c16] = p[i];
-                C_s[wave][g4][c16] = corr;
-            }
-            wave_lds_sync();
-            float cr[GB];
-#pragma unroll
-            for (int h = 0; h < GB; ++h) cr[h] = C_s[wave][g4][h];
-#pragma unroll
-            for (int h = 0; h < GB; ++h)
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) o[h][d] *= cr[h];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float pv[GB];
-#pragma unroll
-                for (int h = 0; h < GB; ++h) pv[h] = P_s[wave][4 * g4 + i][h];
-#pragma unroll
-                for (int r = 0; r < VR; ++r)
-#pragma unroll
-                    for (int j = 0; j < VW; ++j) {
-                        const float vv = raw_at<VW>(b.v[i][r], j);
-#pragma unroll
-                        for (int h = 0; h < GB; ++h) o[h][VW * r + j] = fmaf(pv[h], vv, o[h][VW * r + j]);
-                    }
-            }
-            wave_lds_sync();  // this tile's P/corr reads are done before the next writes
-            // Keep the P.V arithmetic here: without this the compiler sinks it
-            // past the next prefetch, which then has to wait for every load.
-#pragma unroll
-            for (int h = 0; h < GB; ++h)
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) asm volatile("" : "+v"(o[h][d]));
-            asm volatile("" : "+v"(m_run), "+v"(l_run));
-        };
-
-        if constexpr (PIPE) {
-            // Pairs of tiles while two more remain (the loop body has one
-            // shape, no early exit, so its wait counts are exact), then the
-            // last one to three tiles on straight-line paths that load
-            // nothing past the wave's end.
-            int j = 0;
-            for (; j + 3 < my_n; j += 2) {
-                compute_tile(tile_of(j), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 2), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                compute_tile(tile_of(j + 1), b1);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 3), b1);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            const int rest = my_n - j;
-            if (rest == 3) {
-                compute_tile(tile_of(j), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 2), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                compute_tile(tile_of(j + 1), b1);
-                compute_tile(tile_of(j + 2), b0);
-            } else if (rest == 2) {
-                compute_tile(tile_of(j), b0);
-                compute_tile(tile_of(j + 1), b1);
-            } else {
-                compute_tile(tile_of(j), b0);
-            }
-        } else {
-            for (int j = 0; j < my_n; ++j) {
-                load_tile(tile_of(j), b0);
-                compute_tile(tile_of(j), b0);
-            }
-        }
-
-        // Combine the wave's four group streams: M = max of the group maxima;
-        // group g is weighted by exp2(m_g - M), in l and in o.
-        float M = fmaxf(m_run, shfl_xor(m_run, 16));
-        M = fmaxf(M, shfl_xor(M, 32));
-        const float gsc = fast_exp2(m_run - M);
-        float L = l_run * gsc;
-        L += shfl_xor(L, 16);
-        L += shfl_xor(L, 32);
-        if (c16 < GB) C_s[wave][g4][c16] = gsc;
-        wave_lds_sync();
-#pragma unroll
-        for (int h = 0; h < GB; ++h) {
-            const float sc = C_s[wave][g4][h];
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                float x = o[h][d] * sc;
-                x += shfl_xor(x, 16);
-                x += shfl_xor(x, 32);
-                o[h][d] = x;
-            }
-        }
-        if (g4 == 0) {
-#pragma unroll
-            for (int h = 0; h < GB; ++h)
-#pragma unroll
-                for (int r = 0; r < VR; ++r)
-#pragma unroll
-                    for (int j = 0; j < VW; ++j) sm_o[wave][h][v_dim<HD>(c16, r, j)] = o[h][VW * r + j];
-            if (c16 < GB) {
-                sm_m[wave][c16] = M;
-                sm_l[wave][c16] = L;
-            }
-        }
-    } else if (c16 < GB && g4 == 0) {
-        // A wave without tiles contributes nothing: weight exp2(-1e30 - M) = 0.
-        sm_m[wave][c16] = -1e30f;
-        sm_l[wave][c16] = 0.f;
-        for (int d = 0; d < HD; ++d) sm_o[wave][c16][d] = 0.f;
-    }
-    __syncthreads();
-
-    // Combine the WPH waves of each head slot: element (hs, g, d) of the
-    // workgroup; waves hs, hs + HW, ... hold its parts.
-    for (int idx = tid; idx < HW * GB * HD; idx += kDecThreads) {
-        const int e_hs = idx / (GB * HD);
-        const int rem = idx - e_hs * (GB * HD);
-        const int g = rem / HD, d = rem - g * HD;
-        float Mw = sm_m[e_hs][g];
-#pragma unroll
-        for (int ww = 1; ww < WPH; ++ww) Mw = fmaxf(Mw, sm_m[e_hs + ww * HW][g]);
-        float O = 0.f, Lw = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < WPH; ++ww) {
-            const int w = e_hs + ww * HW;
-            const float sc = fast_exp2(sm_m[w][g] - Mw);
-            O = fmaf(sm_o[w][g][d], sc, O);
-            Lw = fmaf(sm_l[w][g], sc, Lw);
-        }
-        const int head = (kvg * HW + e_hs) * a.G + hb * GB + g;
-        const size_t row = (size_t)qi * a.H + head;
-        if (p_u == 1) {
-            a.out[row * HD + d] = O / Lw;
-        } else {
-            const size_t pidx = row * a.P + split;
-            a.part_o[pidx * HD + d] = O;
-            if (d == 0) {
-                a.part_ml[pidx * 2] = Mw;
-                a.part_ml[pidx * 2 + 1] = Lw;
-            }
-        }
-    }
-}
-
-// ------------------------------------------------------------------ host --
-
-struct DecodePlan {
-    int P, tps, n_hblk, gb, hw;
-    int n_main, n_yg;
-    int n_merge, m_cols, m_parts, m_heads, m_slices;
-    size_t ml_bytes, o_bytes;
-    size_t total() const { return ml_bytes + o_bytes; }
-};
 
 // Query heads per wave: the largest divisor of G within the register budget
 // (o holds gb * hd/16 floats per lane, K/V tiles grow with hd) and the 16
@@ -645,46 +82,8 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
     return pl;
 }
 
-template <typename QT, int MODE, int HW>
-static lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, dim3 grid, hipStream_t st) {
-#define LMX_DEC_CASE(HDV, GBV)                                                                     \
-    if (hd == HDV && gb == GBV) {                                                                  \
-        hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE>), grid, dim3(kDecThreads), \
-                           0, st, a);                                                              \
-        return LMX_OK;                                                                             \
-    }
-    LMX_DEC_CASE(64, 1) LMX_DEC_CASE(64, 2) LMX_DEC_CASE(64, 3) LMX_DEC_CASE(64, 4)
-    LMX_DEC_CASE(64, 5) LMX_DEC_CASE(64, 6) LMX_DEC_CASE(64, 7) LMX_DEC_CASE(64, 8)
-    LMX_DEC_CASE(128, 1) LMX_DEC_CASE(128, 2) LMX_DEC_CASE(128, 3) LMX_DEC_CASE(128, 4)
-    LMX_DEC_CASE(128, 5) LMX_DEC_CASE(128, 6)
-    LMX_DEC_CASE(256, 1) LMX_DEC_CASE(256, 2)
-    LMX_DEC_CASE(512, 1)
-#undef LMX_DEC_CASE
-    return LMX_E_UNSUPPORTED;
-}
 
-template <typename QT, int MODE>
-static lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, int hw, dim3 grid,
-                                hipStream_t st) {
-    switch (hw) {
-        case 8: return launch_decode_hw<QT, MODE, 8>(a, hd, gb, grid, st);
-        case 4: return launch_decode_hw<QT, MODE, 4>(a, hd, gb, grid, st);
-        case 2: return launch_decode_hw<QT, MODE, 2>(a, hd, gb, grid, st);
-        default: return launch_decode_hw<QT, MODE, 1>(a, hd, gb, grid, st);
-    }
-}
 
-template <int MODE>
-static lmx_status launch_merge(const DecodeArgs& a, int hd, dim3 grid, hipStream_t st) {
-    switch (hd) {
-        case 64: hipLaunchKernelGGL((attn_merge_kernel<64, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
-        case 128: hipLaunchKernelGGL((attn_merge_kernel<128, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
-        case 256: hipLaunchKernelGGL((attn_merge_kernel<256, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
-        case 512: hipLaunchKernelGGL((attn_merge_kernel<512, MODE>), grid, dim3(kDecThreads), 0, st, a); break;
-        default: return LMX_E_UNSUPPORTED;
-    }
-    return LMX_OK;
-}
 
 // Longest visible range over the batch's queries (attn.wgsl:52-66 maximized
 // over the tokens; O(t) and t is small on this path).
@@ -755,26 +154,17 @@ static lmx_status run(DecodeArgs a, const DecodePlan& pl, int n_q, int hd, lmx_d
     a.m_heads = pl.m_heads;
     a.m_slices = pl.m_slices;
     window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
-    const dim3 grid((unsigned)pl.n_main);
     (void)hipGetLastError();
     lmx_status s;
-#define LMX_DEC_MODE(QT)                                                                     \
-    (mode == kModeLinear    ? launch_decode<QT, kModeLinear>(a, hd, pl.gb, pl.hw, grid, st)  \
-     : mode == kModeGeneral ? launch_decode<QT, kModeGeneral>(a, hd, pl.gb, pl.hw, grid, st) \
-                            : launch_decode<QT, kModeBatched>(a, hd, pl.gb, pl.hw, grid, st))
     if (q_dt == LMX_F32)
-        s = LMX_DEC_MODE(float);
+        s = mode == kModeLinear    ? launch_mode<float, kModeLinear>(a, pl, hd, st)
+            : mode == kModeGeneral ? launch_mode<float, kModeGeneral>(a, pl, hd, st)
+                                   : launch_mode<float, kModeBatched>(a, pl, hd, st);
     else
-        s = LMX_DEC_MODE(f16);
-#undef LMX_DEC_MODE
+        s = mode == kModeLinear    ? launch_mode<f16, kModeLinear>(a, pl, hd, st)
+            : mode == kModeGeneral ? launch_mode<f16, kModeGeneral>(a, pl, hd, st)
+                                   : launch_mode<f16, kModeBatched>(a, pl, hd, st);
     if (s != LMX_OK) return s;
-    if (pl.P > 1) {
-        const dim3 mgrid((unsigned)pl.n_merge);
-        s = mode == kModeLinear    ? launch_merge<kModeLinear>(a, hd, mgrid, st)
-            : mode == kModeGeneral ? launch_merge<kModeGeneral>(a, hd, mgrid, st)
-                                   : launch_merge<kModeBatched>(a, hd, mgrid, st);
-        if (s != LMX_OK) return s;
-    }
     LMX_CHECK_LAUNCH();
     return LMX_OK;
 }

@@ -1,0 +1,6 @@
+// Decode kernels for f16 queries, general addressing (see attn_decode.hpp).
+#include "attn_decode.hpp"
+
+namespace lmx {
+template lmx_status launch_mode<f16, kModeGeneral>(const DecodeArgs&, const DecodePlan&, int, hipStream_t);
+}  // namespace lmx

@@ -36,7 +36,11 @@ struct PrefillArgs {
 };
 
 constexpr int kPfBM = 128;  // query rows per workgroup
-constexpr int kPfBN = 64;   // keys per LDS tile
+// Keys per LDS tile: 64, or 32 at head_dim >= 256 (the register prefetch of
+// the next tile and the o accumulators share one register file).
+template <int HD>
+constexpr int pf_bn() { return HD >= 256 ? 32 : 64; }
+constexpr float kRescaleSlack = 8.f;  // log2 units a running max may lag by
 
 // attn.wgsl:52-66
 __device__ __forceinline__ int vis_lo(int pos, int w) { return (w && pos + 1 > w) ? pos + 1 - w : 0; }
@@ -55,13 +59,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 
 template <typename QT, int HD>
 __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(PrefillArgs a) {
-    constexpr int BN = kPfBN;
+    constexpr int BN = pf_bn<HD>();
+    constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
+    constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
     constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
     constexpr int NB = HD / 32;      // 32-dim output blocks
     constexpr int KPAD = HD + 8;     // K_s row stride (halfs)
     constexpr int VPAD = BN + 4;     // Vt_s row stride (halfs), 8-byte aligned rows
-    __shared__ __attribute__((aligned(16))) f16 K_s[BN * KPAD];
-    __shared__ __attribute__((aligned(16))) f16 Vt_s[HD * VPAD];
+    __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
 
     // ---- which (head, query tile) this workgroup owns
     const int nblk = gridDim.x;
@@ -124,63 +130,87 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[nb][i] = 0.f;
 
-    const int kt_begin = (wg_lo / BN) * BN;
-    for (int kt = kt_begin; kt <= wg_hi; kt += BN) {
-        __syncthreads();  // the previous tile's LDS reads are done
-        // ---- K tile -> K_s[key][dim]; rows outside [wg_lo, wg_hi] are zero
-        constexpr int KCH = HD / 8;  // 16-byte chunks per key row
-        for (int c = tid; c < BN * KCH; c += 256) {
+    // ---- K/V tiles: global -> registers (the next tile's loads are in
+    // flight while the current tile is computed) -> one of two LDS stages.
+    // Rows outside [wg_lo, wg_hi] are zero.
+    constexpr int KCH = HD / 8;                   // 16-byte chunks per key row
+    constexpr int KPT = BN * KCH / 256;           // K chunks per thread
+    constexpr int VPT = (KCH * (BN / 4) + 255) / 256;  // V 4-key groups per thread
+    static_assert(BN * KCH % 256 == 0, "K tile split");
+    f16x8 rk[KPT];
+    f16x8 rv[VPT][4];
+    auto row_src = [&](const f16* cache, const f16* cur, int p) -> const f16* {
+        if (p >= cur_begin) return cur + (size_t)(p - base) * a.kv_dim;
+        const int s = w ? p % w : p;
+        return cache + (size_t)s * a.kv_dim;
+    };
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + 256 * i;
             const int key = c / KCH, col = c - key * KCH;
             const int p = kt + key;
             f16x8 val = {};
-            if (p >= wg_lo && p <= wg_hi) {
-                const f16* src;
-                if (p >= cur_begin) {
-                    src = a.k_cur + (size_t)(p - base) * a.kv_dim;
-                } else {
-                    const int s = w ? p % w : p;
-                    src = a.k + (size_t)s * a.kv_dim;
-                }
-                val = *reinterpret_cast<const f16x8*>(src + kvh * HD + col * 8);
-            }
-            *reinterpret_cast<f16x8*>(&K_s[key * KPAD + col * 8]) = val;
+            if (p >= wg_lo && p <= wg_hi)
+                val = *reinterpret_cast<const f16x8*>(row_src(a.k, a.k_cur, p) + kvh * HD + col * 8);
+            rk[i] = val;
         }
-        // ---- V tile -> Vt_s[dim][key] (transposed), four keys per 8-byte write
-        for (int pr = tid; pr < KCH * (BN / 4); pr += 256) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = tid + 256 * i;
             const int dc = pr % KCH, kg = pr / KCH;
-            f16x8 r[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int p = kt + 4 * kg + u;
-                r[u] = f16x8{};
-                if (p >= wg_lo && p <= wg_hi) {
-                    const f16* src;
-                    if (p >= cur_begin) {
-                        src = a.v_cur + (size_t)(p - base) * a.kv_dim;
-                    } else {
-                        const int s = w ? p % w : p;
-                        src = a.v + (size_t)s * a.kv_dim;
-                    }
-                    r[u] = *reinterpret_cast<const f16x8*>(src + kvh * HD + dc * 8);
-                }
+                f16x8 val = {};
+                if (pr < KCH * (BN / 4) && p >= wg_lo && p <= wg_hi)
+                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + dc * 8);
+                rv[i][u] = val;
             }
+        }
+    };
+    auto stash = [&](int stage) {
+        f16* Ks = K_s + stage * (BN * KPAD);
+        f16* Vts = Vt_s + stage * (HD * VPAD);
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + 256 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            *reinterpret_cast<f16x8*>(&Ks[key * KPAD + col * 8]) = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = tid + 256 * i;
+            if (pr >= KCH * (BN / 4)) continue;
+            const int dc = pr % KCH, kg = pr / KCH;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                *reinterpret_cast<f16x4*>(&Vt_s[(dc * 8 + j) * VPAD + 4 * kg]) =
-                    f16x4{r[0][j], r[1][j], r[2][j], r[3][j]};
+                *reinterpret_cast<f16x4*>(&Vts[(dc * 8 + j) * VPAD + 4 * kg]) =
+                    f16x4{rv[i][0][j], rv[i][1][j], rv[i][2][j], rv[i][3][j]};
         }
-        __syncthreads();
+    };
 
+    const int kt_begin = (wg_lo / BN) * BN;
+    if (kt_begin <= wg_hi) fetch(kt_begin);
+    int stage = 0;
+    for (int kt = kt_begin; kt <= wg_hi; kt += BN, stage ^= 1) {
+        // Stage `stage` was last read two tiles ago, before the barrier of
+        // the previous iteration: writing it now needs no extra barrier.
+        stash(stage);
+        __syncthreads();
+        if (kt + BN <= wg_hi) fetch(kt + BN);
         if (!wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
         const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
+        const f16* Ks = K_s + stage * (BN * KPAD);
+        const f16* Vts = Vt_s + stage * (HD * VPAD);
 
         // ---- S^T = K Q^T, two 32-key blocks
-        f32x16 s[2];
+        f32x16 s[KB];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
-            const f16* krow = &K_s[(kb * 32 + l32) * KPAD + 8 * hh];
+            const f16* krow = &Ks[(kb * 32 + l32) * KPAD + 8 * hh];
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks) {
                 const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + ks * 16);
@@ -192,7 +222,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow.
         float mt = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 float x = s[kb][i] * a.c;
@@ -204,23 +234,28 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
                 mt = fmaxf(mt, x);
             }
         mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float mn = fmaxf(m_run, mt);
-        const float corr = fast_exp2(m_run - mn);
-        m_run = mn;
-        l_run *= corr;
+        // Lazy rescale: the running max moves only when some lane's tile max
+        // exceeds it by more than kRescaleSlack (log2 units), so most tiles
+        // skip the o *= corr pass; p = exp2(x - m_run) stays <= 2^slack.
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack) != 0) {
+            const float mn = fmaxf(m_run, mt);
+            const float corr = fast_exp2(m_run - mn);
+            m_run = mn;
+            l_run *= corr;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+                for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+        }
 
-        // P^T as the B operand of 4 k-steps (16 keys each): step st takes
+        // P^T as the B operand of PST k-steps (16 keys each): step st takes
         // registers 8*(st%2) .. +7 of s[st/2].
-        f16x8 pf[4];
+        f16x8 pf[PST];
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+        for (int st = 0; st < PST; ++st)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p = fast_exp2(s[st / 2][8 * (st % 2) + j] - mn);
+                const float p = fast_exp2(s[st / 2][8 * (st % 2) + j] - m_run);
                 l_run += p;
                 pf[st][j] = (f16)p;
             }
@@ -229,9 +264,9 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         //      16*st' + 4*hh + {0..3} and 16*st' + 8 + 4*hh + {0..3} of the tile.
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const f16* vrow = &Vt_s[(nb * 32 + l32) * VPAD + 4 * hh];
+            const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 4 * hh];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int st = 0; st < PST; ++st) {
                 const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
                 const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
                 const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
