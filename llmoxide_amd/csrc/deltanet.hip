@@ -142,246 +142,429 @@ lmx_status deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt
 // exactly (rows of S are value dims, U/V/O are [C x rows]):
 //
 //   A[t,i] = b_t exp(lg_t - lg_i) k_t.k_i  (i < t),   Tb = (I + A)^-1 diag(b)
-//   U      = Tb (V - diag(exp lg) K S0^T)
-//   O      = diag(exp lg) Q S0^T + P U,   P[t,i] = exp(lg_t - lg_i) q_t.k_i (i <= t)
+//   Z      = V - diag(exp lg) K S0^T,       U = Tb Z
+//   O      = diag(exp lg) Q S0^T + M Z,     M = P Tb,
+//            P[t,i] = exp(lg_t - lg_i) q_t.k_i (i <= t)
 //   S_C    = exp(lg_C) S0 + U^T diag(exp(lg_C - lg)) K
 //
-// Kernel 1 (all (v-head, chunk) pairs in parallel) builds Tb, P and lg.
-// Kernel 2 (one workgroup per (v-head, 16 state rows)) walks the chunks in
-// order, with its 16 rows of S in LDS for the whole call.
+// (M Z = P U; folding Tb into M lets O be formed from Z alongside U.)
+//
+// Every product runs on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), so
+// the arithmetic stays fp32 like the sequential form.  Kernel 1 (one
+// workgroup per (chunk, k-head), all in parallel) builds Tb, M and the decay
+// vectors of every v-head that reads that k-head.  Kernel 2 (one workgroup
+// per (v-head, 16 state rows)) walks the chunks in order with its rows of S
+// in registers.
+//
+// Operand layouts of the 16x16x4 fp32 MFMA, lane l = 16 * lq + lr:
+//   A[i][k]: lane (i = lr, k = lq);  B[k][j]: lane (j = lr, k = lq);
+//   D[i][j]: lane (j = lr), register r holds row i = 4 * lq + r.
+// A contraction may visit its index in any order as long as A and B agree.
+// Over a feature dim d the order used is d = 16 tau + 4 lq + r (step 4 tau + r),
+// so a lane's operands for 4 steps are one contiguous float4 of a row; over a
+// token dim it is t = 16 m + 4 lq + r, which makes a D tile (rows 4 lq + r,
+// column lr) usable as the B operand of the next product without a shuffle.
 
-template <int SD, int C>
-__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
-                                                               float* ws_P, float* ws_lg,
-                                                               int n_chunks) {
-    constexpr int LD = SD + 4;
-    constexpr int PARTS = 256 / C;
-    __shared__ __attribute__((aligned(16))) float Ks[C][LD];
-    __shared__ __attribute__((aligned(16))) float Qs[C][LD];
-    __shared__ float Am[C][C + 1];
-    __shared__ float Tm[C][C + 1];
-    __shared__ float red[PARTS][C];
-    __shared__ float lg[C], bt[C];
-    const int ch = blockIdx.x, hv = blockIdx.y, tid = threadIdx.x;
-    const int c0 = ch * C, nv = min(C, a.n_tok - c0);
-    const int hk = hv % a.n_kh;
-
-    for (int i = tid; i < C * SD / 4; i += 256) {
-        const int r = i / (SD / 4), c4 = i % (SD / 4);
-        f32x4 kq = {0.f, 0.f, 0.f, 0.f}, qq = {0.f, 0.f, 0.f, 0.f};
-        if (r < nv) {
-            const float* row = a.conv + (size_t)(c0 + r) * a.conv_dim + (size_t)hk * SD + 4 * c4;
-            qq = *reinterpret_cast<const f32x4*>(row);
-            kq = *reinterpret_cast<const f32x4*>(row + a.key_dim);
-        }
-        *reinterpret_cast<f32x4*>(&Ks[r][4 * c4]) = kq;
-        *reinterpret_cast<f32x4*>(&Qs[r][4 * c4]) = qq;
-    }
-    if (tid < C) {
-        float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
-        if (tid < nv) {
-            const size_t gi = (size_t)(c0 + tid) * a.n_vh + hv;
-            l = a.ssm_a[hv] * softplus_f(a.alpha[gi] + a.dt_bias[hv]);
-            b = 1.f / (1.f + expf(-a.beta[gi]));
-        }
-        lg[tid] = l;
-        bt[tid] = b;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float s = 0.f;
-        for (int t = 0; t < C; ++t) {
-            s += lg[t];
-            lg[t] = s;
-        }
-    }
-    __syncthreads();
-
-    // Gram matrices: thread (bt_, bi) owns rows t = bt_ + 16u, cols i = bi + 16v.
-    float* Pg = ws_P + ((size_t)hv * n_chunks + ch) * C * C;
-    for (int blk = tid; blk < 16 * 16; blk += 256) {
-        const int tr = blk / 16, ic = blk % 16;
-        constexpr int NU = C / 16;
-        float gkk[NU][NU], gqk[NU][NU];
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int v = 0; v < NU; ++v) gkk[u][v] = gqk[u][v] = 0.f;
-#pragma unroll 2
-        for (int d = 0; d < SD; d += 4) {
-            f32x4 kt[NU], qt[NU], ki[NU];
-#pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                kt[u] = *reinterpret_cast<const f32x4*>(&Ks[tr + 16 * u][d]);
-                qt[u] = *reinterpret_cast<const f32x4*>(&Qs[tr + 16 * u][d]);
-                ki[u] = *reinterpret_cast<const f32x4*>(&Ks[ic + 16 * u][d]);
-            }
-#pragma unroll
-            for (int u = 0; u < NU; ++u)
-#pragma unroll
-                for (int v = 0; v < NU; ++v)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        gkk[u][v] = fmaf(kt[u][e], ki[v][e], gkk[u][v]);
-                        gqk[u][v] = fmaf(qt[u][e], ki[v][e], gqk[u][v]);
-                    }
-        }
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int v = 0; v < NU; ++v) {
-                const int t = tr + 16 * u, i = ic + 16 * v;
-                const float dec = i <= t ? expf(lg[t] - lg[i]) : 0.f;
-                Am[t][i] = i < t ? bt[t] * dec * gkk[u][v] : 0.f;
-                Pg[t * C + i] = gqk[u][v] * dec;
-            }
-    }
-    __syncthreads();
-
-    // T = (I + A)^-1, unit lower triangular, one row at a time:
-    //   T[t][c] = [t == c] - sum_{c <= i < t} A[t][i] T[i][c]
-    const int c = tid % C, part = tid / C;  // 256/C threads per column
-    for (int t = 0; t < C; ++t) {
-        float s = 0.f;
-        if (c < t)
-            for (int i = c + part; i < t; i += PARTS) s = fmaf(Am[t][i], Tm[i][c], s);
-        red[part][c] = s;
-        __syncthreads();
-        if (part == 0) {
-            float tot = 0.f;
-            for (int pp = 0; pp < PARTS; ++pp) tot += red[pp][c];
-            Tm[t][c] = c < t ? -tot : (c == t ? 1.f : 0.f);
-        }
-        __syncthreads();
-    }
-    float* Tg = ws_T + ((size_t)hv * n_chunks + ch) * C * C;
-    for (int i = tid; i < C * C; i += 256) Tg[i] = Tm[i / C][i % C] * bt[i % C];
-    if (tid < C) ws_lg[((size_t)hv * n_chunks + ch) * C + tid] = lg[tid];
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int SD, int C, int R>
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// Per-chunk inputs of a scan wave that are not K or Q (see the scan kernel).
+template <int NM>
+struct ChunkIn {
+    f32x4 v, e;           // V and exp(lg) at tokens 16 m + 4 lq + r
+    f32x4 tb[NM], mm[NM]; // Tb, M row 16 m + lr, columns 16 n + 4 lq + r
+    f32x4 w[NM];          // exp(lg_C - lg) at tokens 16 n + 4 lq + r
+    float gam;            // exp(lg_C)
+};
+
+template <int C>
+struct ChunkSmem {
+    static constexpr int LD = C + 4;  // row stride in floats; keeps float4 rows aligned
+};
+
+// One workgroup per (chunk, k-head).  K K^T and Q K^T are shared by the v-heads
+// hv = hk + u * n_kh (hv % n_kh == hk, deltanet.wgsl:200), so they are formed
+// once, into registers; the decays, the solve and P are per v-head.  LDS holds
+// only A and T (about 35 KB), so four workgroups share a CU and hide each
+// other's latency-bound phases.
+template <int SD, int C>
+__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
+                                                               float* ws_P, float* ws_e,
+                                                               int n_chunks) {
+    constexpr int NT = SD / 16, NM = C / 16, LD = ChunkSmem<C>::LD;
+    constexpr int NTILE = NM * (NM + 1) / 2, TPW = (NTILE + 3) / 4;
+    __shared__ __attribute__((aligned(16))) float As[C * LD];  // strictly lower A
+    __shared__ __attribute__((aligned(16))) float Tm[C * LD];  // (I + A)^-1
+    __shared__ __attribute__((aligned(16))) float Ps[C * LD];  // P
+    __shared__ float lg_w[4][64], b_w[4][64];                  // one copy per wave
+    const int ch = blockIdx.x, hk = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c0 = ch * C, nv = min(C, a.n_tok - c0);
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+    // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
+    // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
+    f32x4 gk[TPW], gq[TPW];
+    int tile_m[TPW], tile_n[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+        int m = 0, n = w + 4 * k;
+        while (n > m) {
+            n -= m + 1;
+            ++m;
+        }
+        tile_m[k] = m;
+        tile_n[k] = n;
+        gk[k] = z4;
+        gq[k] = z4;
+        if (w + 4 * k >= NTILE) continue;
+        const int tm = 16 * m + lr, tn = 16 * n + lr;
+        const bool okm = tm < nv, okn = tn < nv;
+        const float* rm = a.conv + (size_t)(c0 + (okm ? tm : 0)) * a.conv_dim + (size_t)hk * SD + 4 * lq;
+        const float* rn = a.conv + (size_t)(c0 + (okn ? tn : 0)) * a.conv_dim + (size_t)hk * SD +
+                          4 * lq + a.key_dim;
+#pragma unroll
+        for (int h = 0; h < NT; h += 4) {
+            f32x4 qm[4], km[4], kn[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                qm[u] = ld4(rm + 16 * (h + u));
+                km[u] = ld4(rm + a.key_dim + 16 * (h + u));
+                kn[u] = ld4(rn + 16 * (h + u));
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    gk[k] = mfma4(okm ? km[u][r] : 0.f, okn ? kn[u][r] : 0.f, gk[k]);
+                    gq[k] = mfma4(okm ? qm[u][r] : 0.f, okn ? kn[u][r] : 0.f, gq[k]);
+                }
+        }
+    }
+
+    for (int hv = hk; hv < a.n_vh; hv += a.n_kh) {
+        const size_t cb = (size_t)hv * n_chunks + ch;
+        if (hv != hk) __syncthreads();  // the previous head is done with Ps and Tm
+        // Every wave forms the log-decay cumsum and b for lane = token itself.
+        {
+            float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
+            if (lane < nv) {
+                const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
+                l = a.ssm_a[hv] * softplus_f(a.alpha[gi] + a.dt_bias[hv]);
+                b = 1.f / (1.f + expf(-a.beta[gi]));
+            }
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(l, off);
+                if (lane >= off) l += y;
+            }
+            lg_w[w][lane] = l;
+            b_w[w][lane] = b;
+            if (w == 0 && lane < C) {
+                const float lgC = __shfl(l, C - 1);
+                ws_e[cb * 2 * C + lane] = expf(l);
+                ws_e[cb * 2 * C + C + lane] = expf(lgC - l);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        float* Mg = ws_P + cb * C * C;
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) {
+            if (w + 4 * k >= NTILE) continue;
+            const int i = 16 * tile_n[k] + lr;
+            const float li = lg_w[w][i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tile_m[k] + 4 * lq + r;
+                const float dec = i <= t ? expf(lg_w[w][t] - li) : 0.f;
+                As[t * LD + i] = i < t ? b_w[w][t] * dec * gk[k][r] : 0.f;
+                Ps[t * LD + i] = dec * gq[k][r];
+            }
+        }
+        // Blocks of M above the diagonal are zero.
+        for (int idx = tid; idx < NM * NM * 256; idx += 256) {
+            const int t = idx / C, i = idx % C;
+            if ((i >> 4) > (t >> 4)) Mg[idx] = 0.f;
+        }
+        __syncthreads();  // A and P complete
+
+        // (I + A)^-1 by 16x16 blocks.  Diagonal blocks by forward substitution,
+        // lane lr owning column lr of block w:
+        //   T[t][c] = [t == c] - sum_{i < t} A[t][i] T[i][c]
+        if (w < NM) {
+            const int base = 16 * w;
+            float tv[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                float s = t == lr ? 1.f : 0.f;
+                const float* arow = As + (base + t) * LD + base;
+#pragma unroll
+                for (int i = 0; i < t; ++i) s = fmaf(-arow[i], tv[i], s);
+                tv[t] = s;
+            }
+            if (lq == 0)
+#pragma unroll
+                for (int t = 0; t < 16; ++t) Tm[(base + t) * LD + base + lr] = tv[t];
+        }
+        // Off-diagonal blocks level by level:
+        //   T[M][N] = -T[M][M] * sum_{N <= Q < M} A[M][Q] T[Q][N]
+        for (int lev = 1; lev < NM; ++lev) {
+            __syncthreads();
+            if (w < NM - lev) {
+                const int N = w, M = w + lev;
+                f32x4 x = z4;
+                for (int Q = N; Q < M; ++Q) {
+                    const f32x4 av = ld4(As + (16 * M + lr) * LD + 16 * Q + 4 * lq);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        x = mfma4(av[s], Tm[(16 * Q + 4 * lq + s) * LD + 16 * N + lr], x);
+                }
+                const f32x4 tv = ld4(Tm + (16 * M + lr) * LD + 16 * M + 4 * lq);
+                f32x4 y = z4;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) y = mfma4(tv[s], x[s], y);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Tm[(16 * M + 4 * lq + r) * LD + 16 * N + lr] = -y[r];
+            }
+        }
+        __syncthreads();
+        float* Tg = ws_T + cb * C * C;
+        for (int idx = tid; idx < C * C; idx += 256) {
+            const int t = idx / C, i = idx % C;
+            Tg[idx] = i <= t ? Tm[t * LD + i] * b_w[w][i] : 0.f;
+        }
+        // M = P Tb on the blocks at or below the diagonal:
+        //   M[m][n] = sum_{n <= k <= m} P[m][k] T[k][n] diag(b)
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+            if (w + 4 * q >= NTILE) continue;
+            const int m = tile_m[q], n = tile_n[q];
+            const float bc = b_w[w][16 * n + lr];
+            f32x4 acc = z4;
+            for (int k = n; k <= m; ++k) {
+                const f32x4 pv = ld4(Ps + (16 * m + lr) * LD + 16 * k + 4 * lq);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc = mfma4(pv[s], Tm[(16 * k + 4 * lq + s) * LD + 16 * n + lr] * bc, acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Mg[(16 * m + 4 * lq + r) * C + 16 * n + lr] = acc[r];
+        }
+    }
+}
+
+// One workgroup per (v-head, 16 state rows); blockIdx % n_vh == hv, so with
+// n_vh a multiple of 8 the row blocks of a head land on one XCD and share
+// its L2 for K, Q, Tb and P.  Wave w owns token tile w of each chunk (X, Y,
+// U, O) and state columns [16 TPW w, 16 TPW (w + 1)) for the update; the
+// updated columns are exchanged through LDS once per chunk.
+template <int SD, int C>
 __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(DeltaArgs a, const float* ws_T,
                                                                const float* ws_P,
-                                                               const float* ws_lg, int n_chunks) {
-    constexpr int LD = SD + 4;
-    __shared__ __attribute__((aligned(16))) float KQ[2 * C][LD];  // K rows, then Q rows
-    __shared__ __attribute__((aligned(16))) float Ss[R][LD];
-    __shared__ float Tb[C][C + 1];
-    __shared__ float Pm[C][C + 1];
-    __shared__ float XY[2 * C][R + 1];
-    __shared__ float Zs[C][R + 1];
-    __shared__ float Us[C][R + 1];
-    __shared__ float lgs[C];
-    const int tid = threadIdx.x;
-    // blockIdx % 8 == hv % 8: the row blocks of one head share an XCD's L2.
+                                                               const float* ws_e, int n_chunks) {
+    constexpr int NT = SD / 16, NM = C / 16, TPW = NT / 4, LD = ChunkSmem<C>::LD;
+    __shared__ __attribute__((aligned(16))) float Kt[SD * LD];  // K^T of the chunk
+    __shared__ f32x4 Zx[NM * 64];                                // Z tiles, D layout
+    __shared__ f32x4 Ux[NM * 64];                                // U tiles, D layout
+    __shared__ f32x4 Sx[NT * 64];                                // S columns, D layout
+    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hv = blockIdx.x % a.n_vh, rb = blockIdx.x / a.n_vh;
-    const int row0 = rb * R, hk = hv % a.n_kh;
-    float* S_g = a.state + ((size_t)hv * SD + row0) * SD;
+    const int row0 = rb * 16, hk = hv % a.n_kh;
+    // With C = 64 every wave owns a token tile; the constant keeps the loads
+    // out of branches, so their waits count only what each use needs.
+    const bool tok_wave = NM >= 4 || w < NM;
+    const int m = tok_wave ? w : 0;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-    for (int i = tid; i < R * SD / 4; i += 256) {
-        const int j = i / (SD / 4), c4 = i % (SD / 4);
-        *reinterpret_cast<f32x4*>(&Ss[j][4 * c4]) = *reinterpret_cast<const f32x4*>(S_g + (size_t)j * SD + 4 * c4);
-    }
-
-    for (int ch = 0; ch < n_chunks; ++ch) {
-        const int c0 = ch * C, nv = min(C, a.n_tok - c0);
-        __syncthreads();
-        for (int i = tid; i < C * SD / 4; i += 256) {
-            const int r = i / (SD / 4), c4 = i % (SD / 4);
-            f32x4 kq = {0.f, 0.f, 0.f, 0.f}, qq = {0.f, 0.f, 0.f, 0.f};
-            if (r < nv) {
-                const float* row = a.conv + (size_t)(c0 + r) * a.conv_dim + (size_t)hk * SD + 4 * c4;
-                qq = *reinterpret_cast<const f32x4*>(row);
-                kq = *reinterpret_cast<const f32x4*>(row + a.key_dim);
-            }
-            *reinterpret_cast<f32x4*>(&KQ[r][4 * c4]) = kq;
-            *reinterpret_cast<f32x4*>(&KQ[C + r][4 * c4]) = qq;
-        }
-        const float* Tg = ws_T + ((size_t)hv * n_chunks + ch) * C * C;
-        const float* Pg = ws_P + ((size_t)hv * n_chunks + ch) * C * C;
-        for (int i = tid; i < C * C; i += 256) {
-            Tb[i / C][i % C] = Tg[i];
-            Pm[i / C][i % C] = Pg[i];
-        }
-        for (int i = tid; i < C * R; i += 256) {
-            const int t = i / R, j = i % R;
-            Zs[t][j] = t < nv ? a.conv[(size_t)(c0 + t) * a.conv_dim + 2 * (size_t)a.key_dim +
-                                       (size_t)hv * SD + row0 + j]
-                              : 0.f;
-        }
-        if (tid < C) lgs[tid] = ws_lg[((size_t)hv * n_chunks + ch) * C + tid];
-        __syncthreads();
-
-        // XY = [K; Q] S_rows^T
-        for (int it = tid; it < 2 * C * (R / 8); it += 256) {
-            const int r = it / (R / 8), j0 = 8 * (it % (R / 8));
-            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int d = 0; d < SD; d += 4) {
-                const f32x4 x = *reinterpret_cast<const f32x4*>(&KQ[r][d]);
+    // Row j = row0 + lr of S; register u holds columns 16 u + 4 lq + [0, 4).
+    float* srow = a.state + ((size_t)hv * SD + row0 + lr) * SD + 4 * lq;
+    f32x4 S[NT];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const f32x4 s = *reinterpret_cast<const f32x4*>(&Ss[j0 + jj][d]);
-                    acc[jj] = fmaf(x[0], s[0], fmaf(x[1], s[1], fmaf(x[2], s[2], fmaf(x[3], s[3], acc[jj]))));
+    for (int u = 0; u < NT; ++u) S[u] = ld4(srow + 16 * u);
+    f32x4 Sown[TPW];  // this wave's columns 16 (TPW w + j) + 4 lq + r, which it updates
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) Sown[j] = ld4(srow + 16 * (TPW * w + j));
+
+    // Inputs of one chunk.  The next chunk's are loaded during this chunk's
+    // X/Y products: after the MFMAs of column block u, K and Q block u (dead
+    // by then) are reloaded in place and a share of the other loads is issued,
+    // so the vector-memory path is fed at the MFMA pace instead of in one
+    // burst that stalls issue.  The non-K/Q inputs alternate between two
+    // register sets (the loop is unrolled by two), so nothing is copied.
+    f32x4 kr[NT], qr[NT];  // K, Q row 16 m + lr
+    ChunkIn<NM> in0, in1;
+    // A zero the compiler cannot see through: indexing with it keeps uniform
+    // loads on the vector path, counted by vmcnt, instead of the scalar path,
+    // whose counter is shared with LDS and drained at every barrier.
+    int vzero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+
+    // Tokens past the end of the last chunk read row 0 of the chunk instead:
+    // their b is 0, so their rows and columns of Tb are exactly zero, their U
+    // rows are exactly zero, and only finiteness of what they read matters.
+    auto kq_row = [&](int ch) {
+        const int t = 16 * m + lr;
+        return a.conv + (size_t)(ch * C + (t < a.n_tok - ch * C ? t : 0)) * a.conv_dim +
+               (size_t)hk * SD + 4 * lq;
+    };
+    constexpr int NITEM = 6 + 3 * NM;
+    auto fetch_item = [&](int ch, ChunkIn<NM>& d, int k) {
+        const size_t cb = (size_t)hv * n_chunks + ch;
+        const float* eb = ws_e + cb * 2 * C;
+        if (k == 0) {
+            d.gam = eb[C - 1 + vzero];
+        } else if (k == 1) {
+            d.e = ld4(eb + 16 * m + 4 * lq);
+        } else if (k < 6) {
+            const int tv = 16 * m + 4 * lq + (k - 2);
+            const float* vcol = a.conv + 2 * (size_t)a.key_dim + (size_t)hv * SD + row0 + lr;
+            d.v[k - 2] = vcol[(size_t)(ch * C + (tv < a.n_tok - ch * C ? tv : 0)) * a.conv_dim];
+        } else if (k < 6 + NM) {
+            d.tb[k - 6] = ld4(ws_T + (cb * C + 16 * m + lr) * C + 4 * lq + 16 * (k - 6));
+        } else if (k < 6 + 2 * NM) {
+            d.mm[k - 6 - NM] = ld4(ws_P + (cb * C + 16 * m + lr) * C + 4 * lq + 16 * (k - 6 - NM));
+        } else {
+            d.w[k - 6 - 2 * NM] = ld4(eb + C + 16 * (k - 6 - 2 * NM) + 4 * lq);
+        }
+    };
+    auto fetch_all = [&](int ch, ChunkIn<NM>& d) {
+        if (tok_wave) {
+            const float* row = kq_row(ch);
+#pragma unroll
+            for (int u = 0; u < NT; ++u) kr[u] = ld4(row + a.key_dim + 16 * u);
+#pragma unroll
+            for (int u = 0; u < NT; ++u) qr[u] = ld4(row + 16 * u);
+        }
+#pragma unroll
+        for (int k = 0; k < NITEM; ++k)
+            if (tok_wave || k == 0 || k >= 6 + 2 * NM) fetch_item(ch, d, k);
+    };
+
+    auto step = [&](int ch, const ChunkIn<NM>& cur, ChunkIn<NM>& nxt) {
+        const int nv = a.n_tok - ch * C;
+        const int cn = min(ch + 1, n_chunks - 1);
+        f32x4 X = z4, Y = z4;
+        if (tok_wave) {
+            // X = K S^T, Y = Q S^T over d = 16 u + 4 lq + r
+            const float* row = kq_row(cn);
+#pragma unroll
+            for (int u = 0; u < NT; ++u) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    X = mfma4(kr[u][r], S[u][r], X);
+                    Y = mfma4(qr[u][r], S[u][r], Y);
                 }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Kt[(16 * u + 4 * lq + r) * LD + 16 * m + lr] = kr[u][r];
+                kr[u] = ld4(row + a.key_dim + 16 * u);
+                qr[u] = ld4(row + 16 * u);
+                if (u < 2) fetch_item(cn, nxt, u);  // gam, e
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            fetch_item(cn, nxt, 0);  // gam
+        }
+        if (tok_wave) {
+            // Z = V - exp(lg) X
+            f32x4 Z;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Z[r] = cur.v[r] - cur.e[r] * X[r];
+            Zx[m * 64 + lane] = Z;
+        }
+        __syncthreads();
+
+        if (tok_wave) {
+            // U = Tb Z and O = exp(lg) Y + M Z over t = 16 n + 4 lq + r, as two
+            // interleaved chains; blocks above the diagonal of Tb and M are zero.
+            f32x4 U = z4, O;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) O[r] = cur.e[r] * Y[r];
+#pragma unroll
+            for (int n = 0; n < NM; ++n) {
+                const f32x4 zb = Zx[n * 64 + lane];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    U = mfma4(cur.tb[n][s], zb[s], U);
+                    O = mfma4(cur.mm[n][s], zb[s], O);
+                }
+                fetch_item(cn, nxt, 2 + n);  // V
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) XY[r][j0 + jj] = acc[jj];
-        }
-        __syncthreads();
-        // Z = V - exp(lg) X
-        for (int i = tid; i < C * R; i += 256) {
-            const int t = i / R, j = i % R;
-            Zs[t][j] -= expf(lgs[t]) * XY[t][j];
-        }
-        __syncthreads();
-        // U = Tb Z  (Tb lower triangular)
-        for (int i = tid; i < C * R; i += 256) {
-            const int t = i / R, j = i % R;
-            float u = 0.f;
-            for (int k = 0; k <= t; ++k) u = fmaf(Tb[t][k], Zs[k][j], u);
-            Us[t][j] = u;
-        }
-        __syncthreads();
-        // O = exp(lg) Y + P U
-        for (int i = tid; i < C * R; i += 256) {
-            const int t = i / R, j = i % R;
-            float o = expf(lgs[t]) * XY[C + t][j];
-            for (int k = 0; k <= t; ++k) o = fmaf(Pm[t][k], Us[k][j], o);
-            if (t < nv) a.out[(size_t)(c0 + t) * a.d_inner + (size_t)hv * SD + row0 + j] = o * a.scale;
-        }
-        // S_rows = exp(lg_C) S_rows + (U * exp(lg_C - lg))^T K
-        {
-            const float lgC = lgs[C - 1];
-            const float decC = expf(lgC);
-            for (int i = tid; i < R * SD / 4; i += 256) {
-                const int j = i / (SD / 4), d = 4 * (i % (SD / 4));
-                f32x4 s = *reinterpret_cast<const f32x4*>(&Ss[j][d]);
-                s[0] *= decC;
-                s[1] *= decC;
-                s[2] *= decC;
-                s[3] *= decC;
-                for (int t = 0; t < C; ++t) {
-                    const float w = Us[t][j] * expf(lgC - lgs[t]);
-                    const f32x4 k = *reinterpret_cast<const f32x4*>(&KQ[t][d]);
-                    s[0] = fmaf(w, k[0], s[0]);
-                    s[1] = fmaf(w, k[1], s[1]);
-                    s[2] = fmaf(w, k[2], s[2]);
-                    s[3] = fmaf(w, k[3], s[3]);
-                }
-                *reinterpret_cast<f32x4*>(&Ss[j][d]) = s;
+            for (int k = 2 + NM; k < 6; ++k) fetch_item(cn, nxt, k);
+            Ux[m * 64 + lane] = U;
+            float* orow = a.out + (size_t)ch * C * a.d_inner + (size_t)hv * SD + row0 + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * m + 4 * lq + r;
+                if (t < nv) orow[(size_t)t * a.d_inner] = O[r] * a.scale;
             }
+#pragma unroll
+            for (int n = 0; n < NM; ++n) fetch_item(cn, nxt, 6 + n);  // Tb
         }
+        __syncthreads();
+
+        // S <- exp(lg_C) S + (U diag(exp(lg_C - lg)))^T K on this wave's
+        // columns, one chain per column tile, interleaved.
+        f32x4 W[NM];
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            const f32x4 ub = Ux[n * 64 + lane];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) W[n][s] = ub[s] * cur.w[n][s];
+        }
+        f32x4 acc[TPW];
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[j][r] = cur.gam * Sown[j][r];
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            f32x4 kt[TPW];
+#pragma unroll
+            for (int j = 0; j < TPW; ++j) kt[j] = ld4(Kt + (16 * (TPW * w + j) + lr) * LD + 16 * n + 4 * lq);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int j = 0; j < TPW; ++j) acc[j] = mfma4(kt[j][s], W[n][s], acc[j]);
+            // M and exp(lg_C - lg) of the next chunk, spread over the products
+#pragma unroll
+            for (int k = 6 + NM + n; k < NITEM; k += NM)
+                if (tok_wave || k >= 6 + 2 * NM) fetch_item(cn, nxt, k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            Sx[(TPW * w + j) * 64 + lane] = acc[j];
+            Sown[j] = acc[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NT; ++u) S[u] = Sx[u * 64 + lane];
+    };
+
+    fetch_all(0, in0);
+    // Drain the first chunk's loads here: with nothing outstanding on entry,
+    // the waits inside the loop follow the loop body's own issue order.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    int ch = 0;
+    for (; ch + 1 < n_chunks; ch += 2) {
+        step(ch, in0, in1);
+        step(ch + 1, in1, in0);
     }
-    __syncthreads();
-    for (int i = tid; i < R * SD / 4; i += 256) {
-        const int j = i / (SD / 4), c4 = i % (SD / 4);
-        *reinterpret_cast<f32x4*>(S_g + (size_t)j * SD + 4 * c4) = *reinterpret_cast<const f32x4*>(&Ss[j][4 * c4]);
-    }
+    if (ch < n_chunks) step(ch, in0, in1);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) *reinterpret_cast<f32x4*>(srow + 16 * (TPW * w + j)) = Sown[j];
 }
 
 static size_t chunk_ws_floats(const lmx_dop* op, int chunk) {
     const size_t n_chunks = (op->n_tok + chunk - 1) / chunk;
-    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + chunk);
+    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk);
 }
 
 size_t deltanet_chunked_ws(const lmx_dop* op, int chunk) {
@@ -389,13 +572,12 @@ size_t deltanet_chunked_ws(const lmx_dop* op, int chunk) {
 }
 
 template <int SD, int C>
-static void launch_chunked(const DeltaArgs& a, int n_vh, int n_chunks, float* wsT, float* wsP,
-                           float* wsL, hipStream_t st) {
-    constexpr int R = 16;
-    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C>), dim3(n_chunks, n_vh), dim3(256), 0, st, a,
-                       wsT, wsP, wsL, n_chunks);
-    hipLaunchKernelGGL((delta_chunk_scan_kernel<SD, C, R>), dim3(n_vh * (SD / R)), dim3(256), 0, st,
-                       a, wsT, wsP, wsL, n_chunks);
+static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks, float* wsT,
+                           float* wsP, float* wsE, hipStream_t st) {
+    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C>), dim3(n_chunks, n_kh), dim3(256), 0, st, a,
+                       wsT, wsP, wsE, n_chunks);
+    hipLaunchKernelGGL((delta_chunk_scan_kernel<SD, C>), dim3(n_vh * (SD / 16)), dim3(256), 0, st,
+                       a, wsT, wsP, wsE, n_chunks);
 }
 
 lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
@@ -408,14 +590,14 @@ lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* 
     const size_t per = (size_t)op->n_vh * n_chunks;
     float* wsT = static_cast<float*>(ws);
     float* wsP = wsT + per * chunk * chunk;
-    float* wsL = wsP + per * chunk * chunk;
+    float* wsE = wsP + per * chunk * chunk;
     const int sd = (int)op->s_dim;
     (void)hipGetLastError();
-#define LMX_CH(SDV, CV)                                                                   \
-    if (sd == SDV && chunk == CV) {                                                       \
-        launch_chunked<SDV, CV>(a, (int)op->n_vh, n_chunks, wsT, wsP, wsL, st);            \
-        LMX_CHECK_LAUNCH();                                                               \
-        return LMX_OK;                                                                    \
+#define LMX_CH(SDV, CV)                                                                          \
+    if (sd == SDV && chunk == CV) {                                                              \
+        launch_chunked<SDV, CV>(a, (int)op->n_vh, (int)op->n_kh, n_chunks, wsT, wsP, wsE, st);    \
+        LMX_CHECK_LAUNCH();                                                                      \
+        return LMX_OK;                                                                           \
     }
     LMX_CH(128, 64) LMX_CH(128, 32) LMX_CH(128, 16)
     LMX_CH(64, 64) LMX_CH(64, 32) LMX_CH(64, 16)
