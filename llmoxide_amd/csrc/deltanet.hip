@@ -175,7 +175,7 @@ __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<
 template <int NM>
 struct ChunkIn {
     f32x4 v, e;           // V and exp(lg) at tokens 16 m + 4 lq + r
-    f32x4 tb[NM], mm[NM]; // Tb, M row 16 m + lr, columns 16 n + 4 lq + r
+    f32x4 tb[NM], mm[NM]; // Tb, M row 16 m + lr, columns 16 n + 4 lq + r (block (m, n))
     f32x4 w[NM];          // exp(lg_C - lg) at tokens 16 n + 4 lq + r
     float gam;            // exp(lg_C)
 };
@@ -187,24 +187,57 @@ struct ChunkSmem {
 
 // One workgroup per (chunk, k-head).  K K^T and Q K^T are shared by the v-heads
 // hv = hk + u * n_kh (hv % n_kh == hk, deltanet.wgsl:200), so they are formed
-// once, into registers; the decays, the solve and P are per v-head.  LDS holds
-// only A and T (about 35 KB), so four workgroups share a CU and hide each
-// other's latency-bound phases.
+// once, into registers, from K and Q rows staged in LDS with whole-line loads;
+// the decays, the solve and M are per v-head, in LDS that reuses the staging
+// space.  Decays are handled in log2 units (exp2 is the native instruction).
 template <int SD, int C>
 __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
                                                                float* ws_P, float* ws_e,
                                                                int n_chunks) {
-    constexpr int NT = SD / 16, NM = C / 16, LD = ChunkSmem<C>::LD;
+    constexpr int NM = C / 16, LD = ChunkSmem<C>::LD;
     constexpr int NTILE = NM * (NM + 1) / 2, TPW = (NTILE + 3) / 4;
-    __shared__ __attribute__((aligned(16))) float As[C * LD];  // strictly lower A
-    __shared__ __attribute__((aligned(16))) float Tm[C * LD];  // (I + A)^-1
-    __shared__ __attribute__((aligned(16))) float Ps[C * LD];  // P
-    __shared__ float lg_w[4][64], b_w[4][64];                  // one copy per wave
+    constexpr int KLD = SD + 4;            // staged K/Q row stride in floats
+    constexpr int STAGE = 2 * C * KLD;     // K and Q rows of the chunk
+    constexpr int WORK = 3 * C * LD;       // A, T, P
+    __shared__ __attribute__((aligned(16))) float smem[STAGE > WORK ? STAGE : WORK];
+    float* const Ks = smem;
+    float* const Qs = smem + C * KLD;
+    float* const As = smem;               // strictly lower A, later M
+    float* const Tm = smem + C * LD;      // (I + A)^-1
+    float* const Ps = smem + 2 * C * LD;  // P
+    __shared__ __attribute__((aligned(16))) float lg_w[4][64];  // one copy per wave
+    __shared__ __attribute__((aligned(16))) float b_w[4][64];
     const int ch = blockIdx.x, hk = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c0 = ch * C, nv = min(C, a.n_tok - c0);
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+    // alpha and beta of the next v-head, in flight during the work before it
+    float al_n = 0.f, be_n = 0.f;
+    auto ab_fetch = [&](int hv) {
+        if (lane < nv) {
+            const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
+            al_n = a.alpha[gi];
+            be_n = a.beta[gi];
+        }
+    };
+    ab_fetch(hk);
+
+    // Stage the chunk's K and Q rows; rows past the end are zero.
+#pragma unroll
+    for (int j = 0; j < C * SD / 4 / 256; ++j) {
+        const int idx = tid + 256 * j, row = idx / (SD / 4), c4 = idx % (SD / 4);
+        f32x4 q = z4, k = z4;
+        if (row < nv) {
+            const float* src = a.conv + (size_t)(c0 + row) * a.conv_dim + (size_t)hk * SD + 4 * c4;
+            q = ld4(src);
+            k = ld4(src + a.key_dim);
+        }
+        *reinterpret_cast<f32x4*>(Qs + row * KLD + 4 * c4) = q;
+        *reinterpret_cast<f32x4*>(Ks + row * KLD + 4 * c4) = k;
+    }
+    __syncthreads();
 
     // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
     // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
@@ -222,41 +255,32 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
         gk[k] = z4;
         gq[k] = z4;
         if (w + 4 * k >= NTILE) continue;
-        const int tm = 16 * m + lr, tn = 16 * n + lr;
-        const bool okm = tm < nv, okn = tn < nv;
-        const float* rm = a.conv + (size_t)(c0 + (okm ? tm : 0)) * a.conv_dim + (size_t)hk * SD + 4 * lq;
-        const float* rn = a.conv + (size_t)(c0 + (okn ? tn : 0)) * a.conv_dim + (size_t)hk * SD +
-                          4 * lq + a.key_dim;
+        const float* km = Ks + (16 * m + lr) * KLD + 4 * lq;
+        const float* qm = Qs + (16 * m + lr) * KLD + 4 * lq;
+        const float* kn = Ks + (16 * n + lr) * KLD + 4 * lq;
 #pragma unroll
-        for (int h = 0; h < NT; h += 4) {
-            f32x4 qm[4], km[4], kn[4];
+        for (int u = 0; u < SD / 16; ++u) {
+            const f32x4 a4 = ld4(km + 16 * u), q4 = ld4(qm + 16 * u), b4 = ld4(kn + 16 * u);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                qm[u] = ld4(rm + 16 * (h + u));
-                km[u] = ld4(rm + a.key_dim + 16 * (h + u));
-                kn[u] = ld4(rn + 16 * (h + u));
+            for (int r = 0; r < 4; ++r) {
+                gk[k] = mfma4(a4[r], b4[r], gk[k]);
+                gq[k] = mfma4(q4[r], b4[r], gq[k]);
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    gk[k] = mfma4(okm ? km[u][r] : 0.f, okn ? kn[u][r] : 0.f, gk[k]);
-                    gq[k] = mfma4(okm ? qm[u][r] : 0.f, okn ? kn[u][r] : 0.f, gq[k]);
-                }
         }
     }
 
     for (int hv = hk; hv < a.n_vh; hv += a.n_kh) {
         const size_t cb = (size_t)hv * n_chunks + ch;
-        if (hv != hk) __syncthreads();  // the previous head is done with Ps and Tm
-        // Every wave forms the log-decay cumsum and b for lane = token itself.
+        // the staging (first head) or the previous head's A, T, P are no longer read
+        __syncthreads();
+        // Every wave forms the log2-decay cumsum and b for lane = token itself.
         {
             float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
             if (lane < nv) {
-                const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
-                l = a.ssm_a[hv] * softplus_f(a.alpha[gi] + a.dt_bias[hv]);
-                b = 1.f / (1.f + expf(-a.beta[gi]));
+                l = kLog2e * a.ssm_a[hv] * softplus_f(al_n + a.dt_bias[hv]);
+                b = 1.f / (1.f + expf(-be_n));
             }
+            if (hv + a.n_kh < a.n_vh) ab_fetch(hv + a.n_kh);
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float y = __shfl_up(l, off);
@@ -266,12 +290,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
             b_w[w][lane] = b;
             if (w == 0 && lane < C) {
                 const float lgC = __shfl(l, C - 1);
-                ws_e[cb * 2 * C + lane] = expf(l);
-                ws_e[cb * 2 * C + C + lane] = expf(lgC - l);
+                ws_e[cb * 2 * C + lane] = fast_exp2(l);
+                ws_e[cb * 2 * C + C + lane] = fast_exp2(lgC - l);
             }
         }
         __builtin_amdgcn_wave_barrier();
-        float* Mg = ws_P + cb * C * C;
 #pragma unroll
         for (int k = 0; k < TPW; ++k) {
             if (w + 4 * k >= NTILE) continue;
@@ -280,15 +303,10 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * tile_m[k] + 4 * lq + r;
-                const float dec = i <= t ? expf(lg_w[w][t] - li) : 0.f;
+                const float dec = i <= t ? fast_exp2(lg_w[w][t] - li) : 0.f;
                 As[t * LD + i] = i < t ? b_w[w][t] * dec * gk[k][r] : 0.f;
                 Ps[t * LD + i] = dec * gq[k][r];
             }
-        }
-        // Blocks of M above the diagonal are zero.
-        for (int idx = tid; idx < NM * NM * 256; idx += 256) {
-            const int t = idx / C, i = idx % C;
-            if ((i >> 4) > (t >> 4)) Mg[idx] = 0.f;
         }
         __syncthreads();  // A and P complete
 
@@ -332,12 +350,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
             }
         }
         __syncthreads();
-        float* Tg = ws_T + cb * C * C;
-        for (int idx = tid; idx < C * C; idx += 256) {
-            const int t = idx / C, i = idx % C;
-            Tg[idx] = i <= t ? Tm[t * LD + i] * b_w[w][i] : 0.f;
-        }
-        // M = P Tb on the blocks at or below the diagonal:
+        // M = P Tb on the blocks at or below the diagonal, into As (free now):
         //   M[m][n] = sum_{n <= k <= m} P[m][k] T[k][n] diag(b)
 #pragma unroll
         for (int q = 0; q < TPW; ++q) {
@@ -352,7 +365,28 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
                     acc = mfma4(pv[s], Tm[(16 * k + 4 * lq + s) * LD + 16 * n + lr] * bc, acc);
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) Mg[(16 * m + 4 * lq + r) * C + 16 * n + lr] = acc[r];
+            for (int r = 0; r < 4; ++r) As[(16 * m + 4 * lq + r) * LD + 16 * n + lr] = acc[r];
+        }
+        __syncthreads();
+        // Tb and M go out in MFMA A-operand order: block (m, n), lane
+        // l = 16 lq + lr, element e holds row 16 m + lr, column 16 n + 4 lq + e,
+        // so each lane of a scan wave reads its block with one float4 and the
+        // wave reads 1 KB contiguous.  Blocks above the diagonal are zero.
+        float* Tg = ws_T + cb * C * C;
+        float* Mg = ws_P + cb * C * C;
+        for (int q = tid; q < C * C / 4; q += 256) {
+            const int l = q & 63, blk = q >> 6;
+            const int bm = blk / NM, bn = blk % NM;
+            const int t = 16 * bm + (l & 15), i0 = 16 * bn + 4 * (l >> 4);
+            const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
+            f32x4 to, mo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                to[e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
+                mo[e] = bn <= bm ? mv[e] : 0.f;
+            }
+            *reinterpret_cast<f32x4*>(Tg + 4 * q) = to;
+            *reinterpret_cast<f32x4*>(Mg + 4 * q) = mo;
         }
     }
 }
@@ -425,9 +459,9 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(DeltaArgs a, cons
             const float* vcol = a.conv + 2 * (size_t)a.key_dim + (size_t)hv * SD + row0 + lr;
             d.v[k - 2] = vcol[(size_t)(ch * C + (tv < a.n_tok - ch * C ? tv : 0)) * a.conv_dim];
         } else if (k < 6 + NM) {
-            d.tb[k - 6] = ld4(ws_T + (cb * C + 16 * m + lr) * C + 4 * lq + 16 * (k - 6));
+            d.tb[k - 6] = ld4(ws_T + cb * C * C + ((m * NM + (k - 6)) * 64 + lane) * 4);
         } else if (k < 6 + 2 * NM) {
-            d.mm[k - 6 - NM] = ld4(ws_P + (cb * C + 16 * m + lr) * C + 4 * lq + 16 * (k - 6 - NM));
+            d.mm[k - 6 - NM] = ld4(ws_P + cb * C * C + ((m * NM + (k - 6 - NM)) * 64 + lane) * 4);
         } else {
             d.w[k - 6 - 2 * NM] = ld4(eb + C + 16 * (k - 6 - 2 * NM) + 4 * lq);
         }
