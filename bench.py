@@ -225,6 +225,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--only", choices=["headline", "all"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--extras", default="",
+                    help="comma-separated names of the extra configs to run (default: all)")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="after the timed runs, copy a 256 MiB fp32 buffer 3 times: the known-size "
+                         "reference that FETCH_SIZE / WRITE_SIZE counter readings are scaled by")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): this build has no "
@@ -262,6 +267,8 @@ def main():
             ("delta_prefill_T4096_sequential", lambda: bench_delta(lmx, torch, 4096, False)),
             ("delta_decode_1tok", lambda: bench_delta(lmx, torch, 1, False, steps=50, warmup=5)),
         ]:
+            if args.extras and name not in args.extras.split(","):
+                continue
             t0 = time.perf_counter()
             try:
                 extra[name] = fn()
@@ -269,6 +276,14 @@ def main():
                 extra[name] = {"error": repr(e)}
             log(f"{name}: {extra[name]} ({time.perf_counter() - t0:.1f}s)")
             torch.cuda.empty_cache()
+
+    if args.pmc_calibration:
+        a = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
 
     cpu = None if args.skip_cpu else cpu_baseline()
     if cpu:
