@@ -92,21 +92,31 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     const int my_lo = qvalid ? vis_lo(qpos, w) : 1;
     const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
 
-    // Q as the B operand: lane holds Q[qrow][ks*16 + 8*hh + j], j < 8.
+    // Q as the B operand: lane holds c * Q[qrow][ks*16 + 8*hh + j], j < 8, with
+    // c = scale * log2(e) folded in before the f16 rounding (one rounding, as
+    // for Q alone), so the S^T accumulators are already exp2 arguments.
     f16x8 qf[KSTEPS];
     {
         const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * HD + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
+            float x[8];
             if constexpr (sizeof(QT) == 2) {
-                qf[ks] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qoff + ks * 16);
+                const f16x8 q8 = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qoff + ks * 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = (float)q8[j];
             } else {
                 const float* qp = reinterpret_cast<const float*>(a.q) + qoff + ks * 16;
                 const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
                 const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
-                qf[ks] = f16x8{(f16)x0[0], (f16)x0[1], (f16)x0[2], (f16)x0[3],
-                               (f16)x1[0], (f16)x1[1], (f16)x1[2], (f16)x1[3]};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[j] = x0[j];
+                    x[4 + j] = x1[j];
+                }
             }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(x[j] * a.c);
         }
     }
 
@@ -144,7 +154,37 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         const int s = w ? p % w : p;
         return cache + (size_t)s * a.kv_dim;
     };
+    // Fast path for a tile whose rows are all visible to the workgroup, come
+    // from the cache (not k_cur) and map to consecutive slots (no ring wrap
+    // inside the tile): one base pointer, no per-row checks.
+    auto fetch_fast = [&](int kt) -> bool {
+        if (kt < wg_lo || kt + BN - 1 > wg_hi || kt + BN - 1 >= cur_begin) return false;
+        int s0 = kt;
+        if (w) {
+            s0 = kt % w;
+            if (s0 + BN > w) return false;
+        }
+        const f16* kb = a.k + (size_t)s0 * a.kv_dim + kvh * HD;
+        const f16* vb = a.v + (size_t)s0 * a.kv_dim + kvh * HD;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + 256 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            rk[i] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * a.kv_dim + col * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = tid + 256 * i;
+            const int dc = pr % KCH, kg = pr / KCH;
+            if (pr < KCH * (BN / 4))
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    rv[i][u] = *reinterpret_cast<const f16x8*>(vb + (size_t)(4 * kg + u) * a.kv_dim + dc * 8);
+        }
+        return true;
+    };
     auto fetch = [&](int kt) {
+        if (fetch_fast(kt)) return;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + 256 * i;
@@ -225,7 +265,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float x = s[kb][i] * a.c;
+                float x = s[kb][i];
                 if (need_mask) {
                     const int key = kt + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
                     if (key < my_lo || key > my_hi) x = -INFINITY;
@@ -250,15 +290,18 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 
         // P^T as the B operand of PST k-steps (16 keys each): step st takes
         // registers 8*(st%2) .. +7 of s[st/2].
+        // The row sum takes the f16-rounded p, as the P.V product does, two
+        // at a time (v_dot2_f32_f16 against 1).
         f16x8 pf[PST];
+        const f16x2 one2 = {(f16)1.f, (f16)1.f};
 #pragma unroll
-        for (int st = 0; st < PST; ++st)
+        for (int st = 0; st < PST; ++st) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = fast_exp2(s[st / 2][8 * (st % 2) + j] - m_run);
-                l_run += p;
-                pf[st][j] = (f16)p;
-            }
+            for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j] - m_run);
+#pragma unroll
+            for (int j = 0; j < 8; j += 2)
+                l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
+        }
 
         // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
         //      16*st' + 4*hh + {0..3} and 16*st' + 8 + 4*hh + {0..3} of the tile.
