@@ -241,6 +241,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
     constexpr bool PIPE = HD <= 128;
+    // Tiles in flight per wave: as many as the register file allows at two
+    // waves per SIMD (a 16-key tile is 16 K + 16 V registers per lane at
+    // hd 128, 8 + 8 at hd 64).
+    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : (GB <= 4 ? 3 : 2));
     static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
     static_assert(VR * VW == DPL, "V lane layout");
     static_assert(kWaves % HW == 0, "waves per head");
@@ -354,14 +358,14 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
                 qraw[s][0] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qo);
             }
         }
-        // The two prefetches are unconditional (a wave with one tile reads it
-        // twice), so every path into the loop has the same loads in flight and
-        // the compiler's wait counts stay exact.
-        Tile b0, b1;
+        // The DEPTH prefetches are unconditional (a wave with fewer tiles reads
+        // its last one again), so every path into the loop has the same loads
+        // in flight and the compiler's wait counts stay exact.
+        Tile bufs[DEPTH];
         const int last_t = my_n - 1;
         if constexpr (PIPE) {
-            load_tile(tile_of(0), b0);
-            load_tile(tile_of(min(1, last_t)), b1);
+#pragma unroll
+            for (int k = 0; k < DEPTH; ++k) load_tile(tile_of(min(k, last_t)), bufs[k]);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -454,39 +458,40 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         };
 
         if constexpr (PIPE) {
-            // Pairs of tiles while two more remain (the loop body has one
-            // shape, no early exit, so its wait counts are exact), then the
-            // last one to three tiles on straight-line paths that load
-            // nothing past the wave's end.
+            // Rounds of DEPTH tiles while DEPTH more remain: compute a buffer,
+            // refill it with the tile DEPTH ahead (the loop body has one shape
+            // and no early exit, so its wait counts are exact).  Then the last
+            // 1 .. 2 DEPTH - 1 tiles on uniform paths that load nothing past
+            // the wave's end.
             int j = 0;
-            for (; j + 3 < my_n; j += 2) {
-                compute_tile(tile_of(j), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 2), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                compute_tile(tile_of(j + 1), b1);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 3), b1);
-                __builtin_amdgcn_sched_barrier(0);
+            for (; j + 2 * DEPTH - 1 < my_n; j += DEPTH) {
+#pragma unroll
+                for (int k = 0; k < DEPTH; ++k) {
+                    compute_tile(tile_of(j + k), bufs[k]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_tile(tile_of(j + DEPTH + k), bufs[k]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
             const int rest = my_n - j;
-            if (rest == 3) {
-                compute_tile(tile_of(j), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                load_tile(tile_of(j + 2), b0);
-                __builtin_amdgcn_sched_barrier(0);
-                compute_tile(tile_of(j + 1), b1);
-                compute_tile(tile_of(j + 2), b0);
-            } else if (rest == 2) {
-                compute_tile(tile_of(j), b0);
-                compute_tile(tile_of(j + 1), b1);
-            } else {
-                compute_tile(tile_of(j), b0);
+#pragma unroll
+            for (int k = 0; k < DEPTH; ++k) {
+                if (k < rest) {
+                    compute_tile(tile_of(j + k), bufs[k]);
+                    if (DEPTH + k < rest) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        load_tile(tile_of(j + DEPTH + k), bufs[k]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
             }
+#pragma unroll
+            for (int k = 0; k + 1 < DEPTH; ++k)
+                if (DEPTH + k < rest) compute_tile(tile_of(j + DEPTH + k), bufs[k]);
         } else {
             for (int j = 0; j < my_n; ++j) {
-                load_tile(tile_of(j), b0);
-                compute_tile(tile_of(j), b0);
+                load_tile(tile_of(j), bufs[0]);
+                compute_tile(tile_of(j), bufs[0]);
             }
         }
 
