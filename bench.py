@@ -168,6 +168,26 @@ def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5):
     return {"window": window, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
+    """Per-head RMS norm + NeoX RoPE on Q and K, and the f16 KV store, at the
+    C2 shape.  Bytes: q read and written (f32), k and v read (f32), k and v
+    written (f16)."""
+    kv_dim = Hkv * hd
+    q = torch.randn((t, H * hd), device="cuda")
+    k = torch.randn((t, kv_dim), device="cuda")
+    v = torch.randn((t, kv_dim), device="cuda")
+    kc = torch.empty((t, kv_dim), dtype=torch.float16, device="cuda")
+    vc = torch.empty_like(kc)
+    qg = torch.ones(hd, device="cuda")
+    kg = torch.ones(hd, device="cuda")
+    fn = lambda: lmx.attn_prologue(q, k, v, kc, vc, n_heads=H, n_kv_heads=Hkv, head_dim=hd,
+                                   base_pos=0, q_gain=qg, k_gain=kg)
+    ms = time_calls([fn], steps, warmup, torch)
+    nbytes = t * (H * hd * 8 + 2 * kv_dim * 4 + 2 * kv_dim * 2)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"t": t, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def bench_delta(lmx, torch, T, chunked, steps=5, warmup=1):
     n_vh, n_kh, sd = 32, 16, 128
     conv_dim = 2 * n_kh * sd + n_vh * sd
@@ -263,6 +283,8 @@ def main():
                                                            window=1024, scale=1 / 16, steps=5, warmup=1)),
             ("gemma_prefill_global_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,
                                                               scale=1 / 16, steps=5, warmup=1)),
+            ("prologue_prefill_t4096", lambda: bench_prologue(lmx, torch, 4096)),
+            ("prologue_decode_t1", lambda: bench_prologue(lmx, torch, 1, steps=50, warmup=5)),
             ("delta_prefill_T4096_chunked", lambda: bench_delta(lmx, torch, 4096, True)),
             ("delta_prefill_T4096_sequential", lambda: bench_delta(lmx, torch, 4096, False)),
             ("delta_decode_1tok", lambda: bench_delta(lmx, torch, 1, False, steps=50, warmup=5)),

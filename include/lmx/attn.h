@@ -96,9 +96,9 @@ const char *lmx_status_str(lmx_status s);
 /* Library version as 10000*major + 100*minor + patch. */
 int lmx_version(void);
 
-/* Zero a workspace before its first use (a fill kernel, not hipMemsetAsync,
- * so the call may sit inside a captured graph).  Every entry point leaves the
- * workspace's counters at zero when its work completes. */
+/* Zero a workspace (a fill kernel, not hipMemsetAsync, so the call may sit
+ * inside a captured graph).  No entry point needs a zeroed workspace: each
+ * one writes every workspace byte it later reads within the same call. */
 lmx_status lmx_workspace_init(void *ws, size_t ws_bytes, lmx_stream stream);
 
 /* ------------------------------------------------------------------------
@@ -112,6 +112,45 @@ lmx_status lmx_workspace_init(void *ws, size_t ws_bytes, lmx_stream stream);
  */
 lmx_status lmx_kv_append(const lmx_kv_desc *d, const float *k_new, const float *v_new,
                          void *k_cache, void *v_cache, lmx_dtype cache_dt, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Attention prologue.  Replaces, in one launch, the per-head rms_norm calls
+ * (ops.wgsl:49-91), rope / rope_partial (ops.wgsl:269-306, 186-218) and the
+ * two write_cache dispatches (ops.wgsl:323-346) in front of attention,
+ * computing the CPU reference (cpu.rs:286-327; qwen35/cpu.rs:294-304).
+ * For token i at pos = base_pos + i:
+ *   each query head h (q + (i*n_heads + h)*q_stride, its first head_dim
+ *   floats; a qwen35 head's gate half after them is untouched), in place:
+ *     x <- rms_norm(x) * q_gain            (ops.rs:40-59; skipped if q_gain NULL)
+ *     x[0:n_rot] <- rope_neox(x[0:n_rot])  (ops.rs:142-159; skipped if n_rot 0)
+ *   each K head of k_new row i: the same with k_gain;
+ *   each V head of v_new row i: rms_norm(x) without gain when v_norm;
+ *   then the K and V rows are stored as lmx_kv_append stores them (f16 RNE at
+ *   slot(pos); the latest position wins a ring slot).
+ * rope_neox pairs dims (j, j + n_rot/2) with angle
+ *   pos * rope_base^(-2j/n_rot) / factor_j  (factor_j = rope_factors[j], or 1
+ *   when rope_factors is NULL), accumulated in double as the reference does.
+ * head_dim: 64, 128, 256 or 512; n_rot even, <= head_dim; q_stride >= head_dim.
+ * k_new/v_new are read only. */
+typedef struct {
+    uint32_t n_tokens;    /* tokens in the batch                              */
+    uint32_t n_heads;     /* query heads                                      */
+    uint32_t n_kv_heads;  /* K/V heads; kv_dim = n_kv_heads*head_dim           */
+    uint32_t head_dim;
+    uint32_t q_stride;    /* floats from one query head to the next           */
+    uint32_t n_rot;       /* leading dims of each head that rotate (0: none)  */
+    uint32_t base_pos;    /* position of token 0                              */
+    uint32_t window;      /* 0: linear cache; else ring of `window` slots     */
+    uint32_t n_slots;     /* rows allocated in each cache                     */
+    uint32_t v_norm;      /* 1: RMS-normalize V per head (Gemma)              */
+    float rms_eps;
+    float rope_base;
+} lmx_prologue_desc;
+
+lmx_status lmx_attn_prologue(const lmx_prologue_desc *d, float *q, const float *k_new,
+                             const float *v_new, const float *q_gain, const float *k_gain,
+                             const float *rope_factors, void *k_cache, void *v_cache,
+                             lmx_dtype cache_dt, lmx_stream stream);
 
 /* ------------------------------------------------------------------------
  * Attention.  Replaces the scores_pass / softmax_pass / weighted_v dispatch

@@ -8,6 +8,9 @@ reference's dispatch interface for that path, in Python over ``ctypes``:
 this module                reference dispatch it mirrors
 =========================  ==================================================
 ``write_cache``            ``write_cache`` (ops.wgsl:323-346; qwen35.rs:1062-1074)
+``attn_prologue``          per-head ``rms_norm`` + ``rope``/``rope_partial`` on Q
+                           and K (+ V norm) + both ``write_cache``
+                           (ops.wgsl:49-91, 186-218, 269-306, 323-346)
 ``attention``              ``scores_pass``/``softmax_pass``/``weighted_v``
                            (attn.wgsl:84-232; qwen35.rs:1076-1094,
                            forward.rs:988-1011)
@@ -99,14 +102,35 @@ class Dop(ctypes.Structure):
     ]
 
 
+class PrologueDesc(ctypes.Structure):
+    """lmx_prologue_desc: geometry of the norm / rotate / store prologue."""
+    _fields_ = [
+        ("n_tokens", ctypes.c_uint32),
+        ("n_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("q_stride", ctypes.c_uint32),
+        ("n_rot", ctypes.c_uint32),
+        ("base_pos", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("n_slots", ctypes.c_uint32),
+        ("v_norm", ctypes.c_uint32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_base", ctypes.c_float),
+    ]
+
+
 # Every symbol include/lmx/attn.h declares, with its ctypes signature.
 _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
 _PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINTER(Dop)
+_PP = ctypes.POINTER(PrologueDesc)
 SIGNATURES = {
     "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "lmx_version": (ctypes.c_int, []),
     "lmx_workspace_init": (ctypes.c_int, [_VP, _SZ, _VP]),
     "lmx_kv_append": (ctypes.c_int, [_PK, _VP, _VP, _VP, _VP, ctypes.c_int, _VP]),
+    "lmx_attn_prologue": (ctypes.c_int, [_PP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
+                                         _VP]),
     "lmx_attn_workspace_bytes": (_SZ, [_PA]),
     "lmx_attn_fwd": (ctypes.c_int, [_PA, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP, _VP, _VP,
                                     _VP, _SZ, _VP]),
@@ -223,6 +247,27 @@ def write_cache(k_new, v_new, k_cache, v_cache, *, base_pos: int, window: int = 
     rc = lib().lmx_kv_append(ctypes.byref(d), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache),
                              F16, _stream(stream))
     _check("lmx_kv_append", rc)
+
+
+def attn_prologue(q, k_new, v_new, k_cache, v_cache, *, n_heads: int, n_kv_heads: int,
+                  head_dim: int, base_pos: int, q_stride: Optional[int] = None,
+                  n_rot: Optional[int] = None, window: int = 0, v_norm: bool = False,
+                  rms_eps: float = 1e-6, rope_base: float = 1e6, q_gain=None, k_gain=None,
+                  rope_factors=None, stream=None):
+    """Per-head RMS norm (gain), NeoX RoPE over n_rot dims and the f16 KV store,
+    in one launch (cpu.rs:286-327; qwen35/cpu.rs:294-304).  q [t, H*q_stride] f32
+    is updated in place; k_new, v_new [t, kv_dim] f32 go to the caches."""
+    _need_cuda(q, k_new, v_new, k_cache, v_cache, q_gain, k_gain, rope_factors)
+    q_stride = q_stride or head_dim
+    n_rot = head_dim if n_rot is None else n_rot
+    t = k_new.shape[0]
+    d = PrologueDesc(t, n_heads, n_kv_heads, head_dim, q_stride, n_rot, base_pos, window,
+                     k_cache.shape[0], int(bool(v_norm)), rms_eps, rope_base)
+    rc = lib().lmx_attn_prologue(ctypes.byref(d), _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_gain),
+                                 _ptr(k_gain), _ptr(rope_factors), _ptr(k_cache), _ptr(v_cache), F16,
+                                 _stream(stream))
+    _check("lmx_attn_prologue", rc)
+    return q
 
 
 def attention(q, k_cache, v_cache, *, n_heads: int, n_kv_heads: int, head_dim: int,

@@ -34,6 +34,12 @@ lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* 
                             float* state, float* out, int chunk, void* ws, size_t ws_bytes,
                             hipStream_t st);
 
+// prologue.hip
+lmx_status attn_prologue(const lmx_prologue_desc* d, float* q, const float* k_new,
+                         const float* v_new, const float* q_gain, const float* k_gain,
+                         const float* rope_factors, void* k_cache, void* v_cache,
+                         hipStream_t st);
+
 // Queries with at most this many tokens take the split-K path; longer
 // batches take the MFMA tile path.
 constexpr uint32_t kSplitKMaxTokens = 8;
@@ -118,7 +124,7 @@ const char* lmx_status_str(lmx_status s) {
     return "unknown status";
 }
 
-int lmx_version(void) { return 100; }
+int lmx_version(void) { return 101; }
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
@@ -167,6 +173,37 @@ lmx_status lmx_kv_append(const lmx_kv_desc* d, const float* k_new, const float* 
                            d->window);
     LMX_CHECK_LAUNCH();
     return LMX_OK;
+}
+
+lmx_status lmx_attn_prologue(const lmx_prologue_desc* d, float* q, const float* k_new,
+                             const float* v_new, const float* q_gain, const float* k_gain,
+                             const float* rope_factors, void* k_cache, void* v_cache,
+                             lmx_dtype cache_dt, lmx_stream stream) {
+    if (!d || !q || !k_new || !v_new || !k_cache || !v_cache) return LMX_E_NULL;
+    if (cache_dt != LMX_F16) return LMX_E_UNSUPPORTED;
+    if (d->n_tokens == 0 || d->n_heads == 0 || d->n_kv_heads == 0) return LMX_E_SHAPE;
+    const uint32_t hd = d->head_dim;
+    if (hd != 64 && hd != 128 && hd != 256 && hd != 512) return LMX_E_UNSUPPORTED;
+    if (d->n_rot % 2 || d->n_rot > hd || d->q_stride < hd) return LMX_E_SHAPE;
+    if (d->n_rot && !(d->rope_base > 0.f)) return LMX_E_SHAPE;
+    if (!(d->rms_eps >= 0.f)) return LMX_E_SHAPE;
+    const uint64_t end = (uint64_t)d->base_pos + d->n_tokens;
+    if (end >= (1ull << 31)) return LMX_E_CONTEXT;
+    if (d->window == 0) {
+        if (end > d->n_slots) return LMX_E_CONTEXT;
+    } else if (d->n_slots < d->window) {
+        return LMX_E_SHAPE;
+    }
+    if ((uint64_t)d->n_heads * d->q_stride * d->n_tokens >= (1ull << 31) ||
+        (uint64_t)d->n_kv_heads * hd * (end > d->n_slots ? end : d->n_slots) >= (1ull << 31))
+        return LMX_E_SHAPE;
+    for (const void* p : {(const void*)q, (const void*)k_new, (const void*)v_new,
+                          (const void*)q_gain, (const void*)k_gain, (const void*)rope_factors})
+        if (p && !aligned(p, 4)) return LMX_E_ALIGN;
+    for (const void* p : {(const void*)k_cache, (const void*)v_cache})
+        if (!aligned(p, 2)) return LMX_E_ALIGN;
+    return attn_prologue(d, q, k_new, v_new, q_gain, k_gain, rope_factors, k_cache, v_cache,
+                         (hipStream_t)stream);
 }
 
 size_t lmx_attn_workspace_bytes(const lmx_attn_params* p) {

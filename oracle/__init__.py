@@ -62,6 +62,22 @@ class OrcDop(ctypes.Structure):
     ]
 
 
+class OrcPrologue(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", ctypes.c_uint32),
+        ("n_heads", ctypes.c_uint32),
+        ("n_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("q_stride", ctypes.c_uint32),
+        ("n_rot", ctypes.c_uint32),
+        ("base_pos", ctypes.c_uint32),
+        ("window", ctypes.c_uint32),
+        ("v_norm", ctypes.c_uint32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_base", ctypes.c_float),
+    ]
+
+
 _lib = None
 
 
@@ -91,6 +107,9 @@ def lib() -> ctypes.CDLL:
         L.orc_delta_recur.argtypes = [P(OrcDop)] + [f32p] * 7
         L.orc_l2_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
         L.orc_rms_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
+        L.orc_rope_neox.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, f32p,
+                                    ctypes.c_int64]
+        L.orc_attn_prologue.argtypes = [P(OrcPrologue), f32p, f32p, f32p, f32p, f32p, f32p, u16p, u16p]
         _lib = L
     return _lib
 
@@ -217,3 +236,36 @@ def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=
     lib().orc_delta_recur(ctypes.byref(op), _f32p(ssm_a), _f32p(dt_bias), _f32p(alpha),
                           _f32p(beta), _f32p(conv), _f32p(S), _f32p(out))
     return out, S
+
+
+def rope_neox(head, pos, base, factors=None):
+    """NeoX rotation of one head's leading dims (ops.rs:142-159); returns a copy."""
+    h = np.ascontiguousarray(head, np.float32).copy()
+    f = None if factors is None else np.ascontiguousarray(factors, np.float32)
+    lib().orc_rope_neox(_f32p(h), h.size, int(pos), float(base),
+                        None if f is None else _f32p(f), 0 if f is None else f.size)
+    return h
+
+
+def attn_prologue(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, n_slots, q_stride=None,
+                  n_rot=None, window=0, v_norm=False, rms_eps=1e-6, rope_base=1e6, q_gain=None,
+                  k_gain=None, rope_factors=None, k_cache=None, v_cache=None):
+    """Norm / rotate / store of the attention inputs (cpu.rs:286-327;
+    qwen35/cpu.rs:294-304).  q [t, H*q_stride], k and v [t, kv_dim] f32.
+    Returns (q_out, k_cache_bits, v_cache_bits); the caches start as given
+    (f16 bits, [n_slots, kv_dim]) or zero."""
+    q_stride = q_stride or head_dim
+    n_rot = head_dim if n_rot is None else n_rot
+    kv_dim = n_kv_heads * head_dim
+    q = np.ascontiguousarray(q, np.float32).copy()
+    t = q.size // (n_heads * q_stride)
+    k = np.ascontiguousarray(k, np.float32).reshape(t, kv_dim).copy()
+    v = np.ascontiguousarray(v, np.float32).reshape(t, kv_dim).copy()
+    kc = np.zeros((n_slots, kv_dim), np.uint16) if k_cache is None else np.ascontiguousarray(k_cache, np.uint16).copy()
+    vc = np.zeros((n_slots, kv_dim), np.uint16) if v_cache is None else np.ascontiguousarray(v_cache, np.uint16).copy()
+    keep = [None if a is None else np.ascontiguousarray(a, np.float32) for a in (q_gain, k_gain, rope_factors)]
+    p = OrcPrologue(t, n_heads, n_kv_heads, head_dim, q_stride, n_rot, base_pos, window,
+                    int(bool(v_norm)), rms_eps, rope_base)
+    lib().orc_attn_prologue(ctypes.byref(p), _f32p(q), _f32p(k), _f32p(v),
+                            *[None if a is None else _f32p(a) for a in keep], _u16p(kc), _u16p(vc))
+    return q, kc, vc

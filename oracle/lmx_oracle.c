@@ -29,6 +29,14 @@
  *                        torch scaled_dot_product_attention with an explicit
  *                        mask, and by invariants (one visible key -> out = v,
  *                        GQA == head-expanded MHA, constant V -> out = V).
+ *   orc_rope_neox        crates/model/src/ops.rs:142-159, pinned by the ported
+ *                        KATs (ops.rs:225-257) and a float64 closed form.
+ *   orc_attn_prologue    the per-head norm / rotate / store sequence of
+ *                        crates/model/src/cpu.rs:286-327 and
+ *                        crates/model/src/qwen35/cpu.rs:294-304, pinned by a
+ *                        float64 restatement and by invariants (unit RMS,
+ *                        norm-preserving pairs, pos 0 and 1e30 factors leave
+ *                        the head as normalized).
  *   orc_delta_recur      crates/model/src/qwen35/cpu.rs:218-245 (and the GPU
  *                        form deltanet.wgsl:193-239), pinned by a float64
  *                        matrix restatement and by invariants (exact write at
@@ -359,4 +367,73 @@ void orc_rms_norm_rows(float *x, int64_t rows, int64_t dim, float eps) {
         float sc = 1.0f / sqrtf(mean_sq + eps);
         for (int64_t d = 0; d < dim; ++d) v[d] *= sc;
     }
+}
+
+/* ------------------------------------------------------ rope / prologue -- */
+/* ops.rs:142-159: NeoX pairs (i, i + d/2) of the d leading dims of a head.
+ * The angle runs in double exactly as the reference: theta starts at pos and
+ * is multiplied by base^(-2/d) once per pair; factor i (1 when absent)
+ * divides the angle; sin and cos are rounded to float. */
+void orc_rope_neox(float *head, int64_t d, int64_t pos, float base, const float *factors,
+                   int64_t n_factors) {
+    const int64_t half = d / 2;
+    const double theta_scale = pow((double)base, -2.0 / (double)d);
+    double theta = (double)pos;
+    for (int64_t i = 0; i < half; ++i) {
+        const double factor = (factors && i < n_factors) ? (double)factors[i] : 1.0;
+        const double angle = theta / factor;
+        const float sn = (float)sin(angle), cs = (float)cos(angle);
+        const float x0 = head[i], x1 = head[i + half];
+        head[i] = x0 * cs - x1 * sn;
+        head[i + half] = x0 * sn + x1 * cs;
+        theta *= theta_scale;
+    }
+}
+
+typedef struct {
+    uint32_t n_tokens, n_heads, n_kv_heads, head_dim;
+    uint32_t q_stride;   /* floats from one query head to the next (>= head_dim) */
+    uint32_t n_rot;      /* leading dims of each head that rotate (even)       */
+    uint32_t base_pos, window;
+    uint32_t v_norm;     /* 1: RMS-normalize V per head, no gain               */
+    float rms_eps, rope_base;
+} orc_prologue;
+
+/* ops.rs:40-47 then the gain multiply of ops.rs:53-59 (gain may be NULL). */
+static void orc_rms_norm_mul(float *x, int64_t n, const float *gain, float eps) {
+    float acc = 0.0f;
+    for (int64_t d = 0; d < n; ++d) acc += x[d] * x[d];
+    const float mean_sq = acc / (float)n;
+    const float sc = 1.0f / sqrtf(mean_sq + eps);
+    for (int64_t d = 0; d < n; ++d) x[d] *= sc;
+    if (gain)
+        for (int64_t d = 0; d < n; ++d) x[d] *= gain[d];
+}
+
+/* cpu.rs:286-327 / qwen35/cpu.rs:294-304: per query head (stride q_stride,
+ * first head_dim floats) RMS norm times q_gain then NeoX rope over n_rot dims
+ * at pos = base_pos + token; per K head the same with k_gain; per V head an
+ * RMS norm without gain when v_norm; then K and V rows go to the f16 caches
+ * at slot(pos) (orc_write_cache).  A NULL gain skips that tensor's norm.
+ * q is updated in place; k and v are scratch copies the caller owns. */
+void orc_attn_prologue(const orc_prologue *p, float *q, float *k, float *v, const float *q_gain,
+                       const float *k_gain, const float *rope_factors, uint16_t *k_cache,
+                       uint16_t *v_cache) {
+    const int64_t hd = p->head_dim, kv_dim = (int64_t)p->n_kv_heads * hd;
+    for (int64_t i = 0; i < p->n_tokens; ++i) {
+        const int64_t pos = (int64_t)p->base_pos + i;
+        for (int64_t h = 0; h < p->n_heads; ++h) {
+            float *head = q + (i * p->n_heads + h) * (int64_t)p->q_stride;
+            if (q_gain) orc_rms_norm_mul(head, hd, q_gain, p->rms_eps);
+            if (p->n_rot) orc_rope_neox(head, p->n_rot, pos, p->rope_base, rope_factors, p->n_rot / 2);
+        }
+        for (int64_t h = 0; h < p->n_kv_heads; ++h) {
+            float *head = k + i * kv_dim + h * hd;
+            if (k_gain) orc_rms_norm_mul(head, hd, k_gain, p->rms_eps);
+            if (p->n_rot) orc_rope_neox(head, p->n_rot, pos, p->rope_base, rope_factors, p->n_rot / 2);
+            if (p->v_norm) orc_rms_norm_mul(v + i * kv_dim + h * hd, hd, NULL, p->rms_eps);
+        }
+    }
+    orc_write_cache(p->n_tokens, kv_dim, p->base_pos, p->window, k, k_cache);
+    orc_write_cache(p->n_tokens, kv_dim, p->base_pos, p->window, v, v_cache);
 }

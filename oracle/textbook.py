@@ -128,3 +128,56 @@ def delta_chunked(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, chunk, ssm_a=None,
             S0 = gam[-1] * S0 + (U * np.exp(lg[-1] - lg)[:, None]).T @ Kc
         S[hv] = S0
     return out, S.reshape(-1)
+
+
+def rope_neox(head, pos, base, factors=None):
+    """NeoX rotation in closed form, float64: pair i is rotated by
+    pos * base^(-2i/d) / factor_i (ops.rs:142-159)."""
+    h = np.asarray(head, np.float64).copy()
+    d = h.size
+    half = d // 2
+    i = np.arange(half, dtype=np.float64)
+    f = np.ones(half) if factors is None else np.asarray(factors, np.float64)[:half]
+    ang = pos * np.power(float(base), -2.0 * i / d) / f
+    c, s = np.cos(ang), np.sin(ang)
+    x0, x1 = h[:half].copy(), h[half:2 * half].copy()
+    h[:half] = x0 * c - x1 * s
+    h[half:2 * half] = x0 * s + x1 * c
+    return h
+
+
+def attn_prologue(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, q_stride=None, n_rot=None,
+                  v_norm=False, rms_eps=1e-6, rope_base=1e6, q_gain=None, k_gain=None,
+                  rope_factors=None):
+    """Float64 restatement of the per-head norm and rotation (cpu.rs:286-327;
+    qwen35/cpu.rs:294-304).  Returns (q_out, k_out, v_out) before the f16 store."""
+    q_stride = q_stride or head_dim
+    n_rot = head_dim if n_rot is None else n_rot
+    q = np.asarray(q, np.float64).reshape(-1, n_heads, q_stride).copy()
+    t = q.shape[0]
+    k = np.asarray(k, np.float64).reshape(t, n_kv_heads, head_dim).copy()
+    v = np.asarray(v, np.float64).reshape(t, n_kv_heads, head_dim).copy()
+
+    def rms(x, gain):
+        x = x / np.sqrt(np.mean(x * x) + rms_eps)
+        return x if gain is None else x * np.asarray(gain, np.float64)
+
+    for i in range(t):
+        pos = base_pos + i
+        for h in range(n_heads):
+            head = q[i, h, :head_dim]
+            if q_gain is not None:
+                head = rms(head, q_gain)
+            if n_rot:
+                head[:n_rot] = rope_neox(head[:n_rot], pos, rope_base, rope_factors)
+            q[i, h, :head_dim] = head
+        for h in range(n_kv_heads):
+            head = k[i, h]
+            if k_gain is not None:
+                head = rms(head, k_gain)
+            if n_rot:
+                head[:n_rot] = rope_neox(head[:n_rot], pos, rope_base, rope_factors)
+            k[i, h] = head
+            if v_norm:
+                v[i, h] = rms(v[i, h], None)
+    return q.reshape(t, -1), k.reshape(t, -1), v.reshape(t, -1)

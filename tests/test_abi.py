@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 11
+    assert len(names) == 12
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = lmx.lib()
-    assert L.lmx_version() == 100
+    assert L.lmx_version() == 101
     for s in lmx.Status:
         assert L.lmx_status_str(int(s))
     assert L.lmx_status_str(999) == b"unknown status"
@@ -144,3 +144,42 @@ def test_deltanet_validation():
     assert L.lmx_deltanet_recur(ctypes.byref(op2), *args, None) == lmx.Status.E_SHAPE
     assert L.lmx_deltanet_chunked(ctypes.byref(op), *args, 48, None, 0, None) == lmx.Status.E_SHAPE
     assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), 48) == 0
+
+
+def _pro(**kw):
+    base = dict(n_tokens=4, n_heads=32, n_kv_heads=8, head_dim=128, q_stride=128, n_rot=128,
+                base_pos=0, window=0, n_slots=16, v_norm=0, rms_eps=1e-6, rope_base=1e6)
+    base.update(kw)
+    return lmx.PrologueDesc(*[base[f] for f, _ in lmx.PrologueDesc._fields_])
+
+
+def _pcall(d, q=FAKE, k=FAKE, v=FAKE, qg=None, kg=None, fac=None, kc=FAKE, vc=FAKE, dt=lmx.F16):
+    return lmx.lib().lmx_attn_prologue(None if d is None else ctypes.byref(d), q, k, v, qg, kg, fac,
+                                       kc, vc, dt, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n_tokens=0), lmx.Status.E_SHAPE),
+    (dict(n_kv_heads=0), lmx.Status.E_SHAPE),
+    (dict(head_dim=96, q_stride=96, n_rot=96), lmx.Status.E_UNSUPPORTED),
+    (dict(n_rot=63), lmx.Status.E_SHAPE),
+    (dict(n_rot=256), lmx.Status.E_SHAPE),
+    (dict(q_stride=64), lmx.Status.E_SHAPE),
+    (dict(rope_base=0.0), lmx.Status.E_SHAPE),
+    (dict(rms_eps=float("nan")), lmx.Status.E_SHAPE),
+    (dict(base_pos=13), lmx.Status.E_CONTEXT),
+    (dict(window=32, n_slots=16), lmx.Status.E_SHAPE),
+])
+def test_prologue_rejects_bad_geometry(kw, code):
+    assert _pcall(_pro(**kw)) == code
+
+
+def test_prologue_rejects_bad_pointers_and_dtypes():
+    d = _pro()
+    assert _pcall(None) == lmx.Status.E_NULL
+    for name in ("q", "k", "v", "kc", "vc"):
+        assert _pcall(d, **{name: None}) == lmx.Status.E_NULL, name
+    assert _pcall(d, dt=lmx.F32) == lmx.Status.E_UNSUPPORTED
+    assert _pcall(d, q=FAKE + 2) == lmx.Status.E_ALIGN
+    assert _pcall(d, qg=FAKE + 1) == lmx.Status.E_ALIGN
+    assert _pcall(d, kc=FAKE + 1) == lmx.Status.E_ALIGN
