@@ -188,6 +188,31 @@ def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
     return {"t": t, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_delta_io(lmx, torch, T, which, steps=20, warmup=3):
+    """Delta-net front (conv + SiLU + window + q/k L2 norm) or back (gated RMS
+    norm) at C5.  Bytes: front reads x and writes conv_out (f32 [T, 8192]),
+    plus taps and window; back reads o and z and writes o (f32 [T, 4096])."""
+    n_vh, n_kh, sd, K = 32, 16, 128, 4
+    key_dim, d_inner = n_kh * sd, n_vh * sd
+    conv_dim = 2 * key_dim + d_inner
+    if which == "front":
+        x = torch.randn((T, conv_dim), device="cuda")
+        taps = torch.randn((conv_dim, K), device="cuda")
+        st = torch.zeros((K - 1, conv_dim), device="cuda")
+        out = torch.empty_like(x)
+        fn = lambda: lmx.delta_front(x, taps, st, out, key_dim=key_dim, s_dim=sd)
+        nbytes = 2 * T * conv_dim * 4 + conv_dim * K * 4 + 2 * (K - 1) * conv_dim * 4
+    else:
+        o = torch.randn((T, d_inner), device="cuda")
+        z = torch.randn((T, d_inner), device="cuda")
+        w = torch.ones(sd, device="cuda")
+        fn = lambda: lmx.delta_back(o, z, w, n_vh=n_vh, s_dim=sd)
+        nbytes = 3 * T * d_inner * 4 + sd * 4
+    ms = time_calls([fn], steps, warmup, torch)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"T": T, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def bench_delta(lmx, torch, T, chunked, steps=5, warmup=1):
     n_vh, n_kh, sd = 32, 16, 128
     conv_dim = 2 * n_kh * sd + n_vh * sd
@@ -288,6 +313,8 @@ def main():
             ("delta_prefill_T4096_chunked", lambda: bench_delta(lmx, torch, 4096, True)),
             ("delta_prefill_T4096_sequential", lambda: bench_delta(lmx, torch, 4096, False)),
             ("delta_decode_1tok", lambda: bench_delta(lmx, torch, 1, False, steps=50, warmup=5)),
+            ("delta_front_T4096", lambda: bench_delta_io(lmx, torch, 4096, "front")),
+            ("delta_back_T4096", lambda: bench_delta_io(lmx, torch, 4096, "back")),
         ]:
             if args.extras and name not in args.extras.split(","):
                 continue

@@ -227,6 +227,45 @@ lmx_status lmx_deltanet_chunked(const lmx_dop *op, const float *ssm_a, const flo
                                 float *state, float *out, int32_t chunk, void *ws,
                                 size_t ws_bytes, lmx_stream stream);
 
+/* ------------------------------------------------------------------------
+ * Delta-net front.  Replaces the conv_silu, conv_shift, conv_commit and
+ * l2norm_qk dispatches (deltanet.wgsl:54-173, recorded at qwen35.rs:928-958)
+ * with one launch, computing the CPU reference (qwen35/cpu.rs:193-216):
+ *   conv_out[i][c] = silu(x[i][c]*taps[c][K-1] + sum_{j<K-1} w_j[c]*taps[c][j])
+ * where w_j is row j of the window [conv_state | x] as seen by token i (the
+ * K-1 rows before it, oldest first), silu(a) = a/(1+exp(-a)) (ops.rs:175-178);
+ * then each q and k head (channels [0, 2*key_dim) in heads of s_dim) is
+ * L2-normalized, x / max(||x||, eps) (ops.rs:197-203).  conv_state ([K-1,
+ * conv_dim], oldest first) becomes the last K-1 rows of [conv_state | x].
+ * conv_out [n_tok, conv_dim] is what lmx_deltanet_recur/_chunked read.
+ * conv_dim a multiple of 128; s_dim 64 or 128; 2 <= kernel <= 8. */
+typedef struct {
+    uint32_t n_tok;       /* tokens in the batch                              */
+    uint32_t conv_dim;    /* channels: q (key_dim) | k (key_dim) | v          */
+    uint32_t key_dim;     /* n_kh * s_dim                                     */
+    uint32_t s_dim;       /* head size of the q/k L2 norm                     */
+    uint32_t kernel;      /* conv taps per channel (4 in qwen35)              */
+    float eps;            /* floor of the L2 norm                             */
+} lmx_delta_front_desc;
+
+lmx_status lmx_deltanet_front(const lmx_delta_front_desc *d, const float *x, const float *taps,
+                              float *conv_state, float *conv_out, lmx_stream stream);
+
+/* Delta-net back.  Replaces the rms_norm + mul_silu pair after the
+ * recurrence (qwen35.rs:968-986), computing qwen35/cpu.rs:250-259 in place:
+ * per token and v-head, o <- rms_norm(o) * w * silu(z), with rms_norm as
+ * ops.rs:40-47 (eps inside the root).  o, z [n_tok, n_vh*s_dim]; w [s_dim];
+ * s_dim 64, 128 or 256. */
+typedef struct {
+    uint32_t n_tok;
+    uint32_t n_vh;
+    uint32_t s_dim;
+    float eps;
+} lmx_delta_back_desc;
+
+lmx_status lmx_deltanet_back(const lmx_delta_back_desc *d, float *o, const float *z,
+                             const float *w, lmx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

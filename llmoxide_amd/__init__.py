@@ -18,6 +18,10 @@ this module                reference dispatch it mirrors
 ``delta_recur``            ``delta_recur`` (deltanet.wgsl:193-239;
                            qwen35.rs:960-965)
 ``delta_chunked``          chunked prefill form of ``delta_recur``
+``delta_front``            ``conv_silu``/``conv_shift``/``conv_commit``/
+                           ``l2norm_qk`` (deltanet.wgsl:54-173)
+``delta_back``             ``rms_norm`` + ``mul_silu`` after the recurrence
+                           (qwen35.rs:968-986)
 =========================  ==================================================
 
 Tensors are torch tensors on a ROCm device (torch provides device memory and
@@ -120,10 +124,33 @@ class PrologueDesc(ctypes.Structure):
     ]
 
 
+class DeltaFrontDesc(ctypes.Structure):
+    """lmx_delta_front_desc: the conv / window / q-k norm front of the delta-net."""
+    _fields_ = [
+        ("n_tok", ctypes.c_uint32),
+        ("conv_dim", ctypes.c_uint32),
+        ("key_dim", ctypes.c_uint32),
+        ("s_dim", ctypes.c_uint32),
+        ("kernel", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class DeltaBackDesc(ctypes.Structure):
+    """lmx_delta_back_desc: the gated RMS norm after the recurrence."""
+    _fields_ = [
+        ("n_tok", ctypes.c_uint32),
+        ("n_vh", ctypes.c_uint32),
+        ("s_dim", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+    ]
+
+
 # Every symbol include/lmx/attn.h declares, with its ctypes signature.
 _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
 _PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINTER(Dop)
 _PP = ctypes.POINTER(PrologueDesc)
+_PF, _PB = ctypes.POINTER(DeltaFrontDesc), ctypes.POINTER(DeltaBackDesc)
 SIGNATURES = {
     "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "lmx_version": (ctypes.c_int, []),
@@ -138,6 +165,8 @@ SIGNATURES = {
     "lmx_attn_decode_batched": (ctypes.c_int, [_PA, _I32, _I32, _VP, _VP, _VP, _VP, ctypes.c_int,
                                                ctypes.c_int, _VP, _VP, _SZ, _VP]),
     "lmx_deltanet_recur": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "lmx_deltanet_front": (ctypes.c_int, [_PF, _VP, _VP, _VP, _VP, _VP]),
+    "lmx_deltanet_back": (ctypes.c_int, [_PB, _VP, _VP, _VP, _VP]),
     "lmx_deltanet_chunked_workspace_bytes": (_SZ, [_PD, _I32]),
     "lmx_deltanet_chunked": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I32, _VP, _SZ,
                                             _VP]),
@@ -376,3 +405,29 @@ def delta_chunked(conv, alpha, beta, state, ssm_a, dt_bias, *, n_vh, n_kh, s_dim
                                     ws_bytes, _stream(stream))
     _check("lmx_deltanet_chunked", rc)
     return out
+
+
+def delta_front(x, taps, conv_state, conv_out=None, *, key_dim: int, s_dim: int,
+                eps: float = 1e-6, stream=None):
+    """Causal depthwise conv + SiLU, conv-window update and q/k L2 norm
+    (qwen35/cpu.rs:193-216).  x [t, conv_dim], taps [conv_dim, kernel],
+    conv_state [kernel-1, conv_dim] (updated).  Returns conv_out [t, conv_dim]."""
+    torch = _torch()
+    _need_cuda(x, taps, conv_state, conv_out)
+    t, conv_dim = x.shape
+    if conv_out is None:
+        conv_out = torch.empty_like(x)
+    d = DeltaFrontDesc(t, conv_dim, key_dim, s_dim, taps.shape[-1], eps)
+    rc = lib().lmx_deltanet_front(ctypes.byref(d), _ptr(x), _ptr(taps), _ptr(conv_state),
+                                  _ptr(conv_out), _stream(stream))
+    _check("lmx_deltanet_front", rc)
+    return conv_out
+
+
+def delta_back(o, z, w, *, n_vh: int, s_dim: int, eps: float = 1e-6, stream=None):
+    """Gated RMS norm (qwen35/cpu.rs:250-259), in place on o [t, n_vh*s_dim]."""
+    _need_cuda(o, z, w)
+    d = DeltaBackDesc(o.shape[0], n_vh, s_dim, eps)
+    rc = lib().lmx_deltanet_back(ctypes.byref(d), _ptr(o), _ptr(z), _ptr(w), _stream(stream))
+    _check("lmx_deltanet_back", rc)
+    return o

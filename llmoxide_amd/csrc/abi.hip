@@ -40,6 +40,12 @@ lmx_status attn_prologue(const lmx_prologue_desc* d, float* q, const float* k_ne
                          const float* rope_factors, void* k_cache, void* v_cache,
                          hipStream_t st);
 
+// deltanet_io.hip
+lmx_status deltanet_front(const lmx_delta_front_desc* d, const float* x, const float* taps,
+                          float* conv_state, float* conv_out, hipStream_t st);
+lmx_status deltanet_back(const lmx_delta_back_desc* d, float* o, const float* z, const float* w,
+                         hipStream_t st);
+
 // Queries with at most this many tokens take the split-K path; longer
 // batches take the MFMA tile path.
 constexpr uint32_t kSplitKMaxTokens = 8;
@@ -124,7 +130,7 @@ const char* lmx_status_str(lmx_status s) {
     return "unknown status";
 }
 
-int lmx_version(void) { return 101; }
+int lmx_version(void) { return 102; }
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
@@ -307,6 +313,37 @@ lmx_status lmx_deltanet_chunked(const lmx_dop* op, const float* ssm_a, const flo
     }
     return deltanet_chunked(op, ssm_a, dt_bias, alpha, beta, conv, state, out, chunk, ws, ws_bytes,
                             (hipStream_t)stream);
+}
+
+lmx_status lmx_deltanet_front(const lmx_delta_front_desc* d, const float* x, const float* taps,
+                              float* conv_state, float* conv_out, lmx_stream stream) {
+    if (!d || !x || !taps || !conv_state || !conv_out) return LMX_E_NULL;
+    if (d->n_tok == 0 || d->conv_dim == 0 || d->conv_dim % 128) return LMX_E_SHAPE;
+    if (d->s_dim != 64 && d->s_dim != 128) return LMX_E_UNSUPPORTED;
+    if (d->key_dim == 0 || d->key_dim % d->s_dim || 2ull * d->key_dim > d->conv_dim) return LMX_E_SHAPE;
+    if (d->kernel < 2 || d->kernel > 8) return LMX_E_UNSUPPORTED;
+    if (!(d->eps >= 0.f) || d->eps == INFINITY) return LMX_E_SHAPE;
+    if ((uint64_t)d->n_tok * d->conv_dim >= (1ull << 31)) return LMX_E_SHAPE;
+    for (const void* p : {(const void*)x, (const void*)taps, (const void*)conv_state,
+                          (const void*)conv_out})
+        if (!aligned(p, 4)) return LMX_E_ALIGN;
+    // the batch rows are read by later tokens' taps: the output must not overlay them
+    const char *xb = (const char*)x, *ob = (const char*)conv_out;
+    const size_t bytes = (size_t)d->n_tok * d->conv_dim * sizeof(float);
+    if (ob < xb + bytes && xb < ob + bytes) return LMX_E_SHAPE;
+    return deltanet_front(d, x, taps, conv_state, conv_out, (hipStream_t)stream);
+}
+
+lmx_status lmx_deltanet_back(const lmx_delta_back_desc* d, float* o, const float* z,
+                             const float* w, lmx_stream stream) {
+    if (!d || !o || !z || !w) return LMX_E_NULL;
+    if (d->n_tok == 0 || d->n_vh == 0) return LMX_E_SHAPE;
+    if (d->s_dim != 64 && d->s_dim != 128 && d->s_dim != 256) return LMX_E_UNSUPPORTED;
+    if (!(d->eps >= 0.f) || d->eps == INFINITY) return LMX_E_SHAPE;
+    if ((uint64_t)d->n_tok * d->n_vh * d->s_dim >= (1ull << 31)) return LMX_E_SHAPE;
+    for (const void* p : {(const void*)o, (const void*)z, (const void*)w})
+        if (!aligned(p, 4)) return LMX_E_ALIGN;
+    return deltanet_back(d, o, z, w, (hipStream_t)stream);
 }
 
 }  // extern "C"

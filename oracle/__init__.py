@@ -110,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.orc_rope_neox.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, f32p,
                                     ctypes.c_int64]
         L.orc_attn_prologue.argtypes = [P(OrcPrologue), f32p, f32p, f32p, f32p, f32p, f32p, u16p, u16p]
+        L.orc_delta_front.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_float] + [f32p] * 4
+        L.orc_delta_back.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_float] + [f32p] * 3
         _lib = L
     return _lib
 
@@ -269,3 +271,29 @@ def attn_prologue(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, n_slots, 
     lib().orc_attn_prologue(ctypes.byref(p), _f32p(q), _f32p(k), _f32p(v),
                             *[None if a is None else _f32p(a) for a in keep], _u16p(kc), _u16p(vc))
     return q, kc, vc
+
+
+def delta_front(x, taps, state, *, key_dim, s_dim, eps=1e-6):
+    """Causal depthwise conv + SiLU, conv-window shift and q/k L2 norm of the
+    delta-net input (qwen35/cpu.rs:193-216).  x [t, conv_dim], taps
+    [conv_dim, kernel], state [kernel-1, conv_dim].  Returns (conv_out, state_new)."""
+    x = np.ascontiguousarray(x, np.float32)
+    t, conv_dim = x.shape
+    taps = np.ascontiguousarray(taps, np.float32).reshape(conv_dim, -1)
+    kernel = taps.shape[1]
+    st = np.ascontiguousarray(state, np.float32).reshape(kernel - 1, conv_dim).copy()
+    out = np.zeros_like(x)
+    lib().orc_delta_front(t, conv_dim, key_dim, s_dim, kernel, eps, _f32p(x), _f32p(taps), _f32p(st),
+                          _f32p(out))
+    return out, st
+
+
+def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):
+    """Gated RMS norm of the delta-net output (qwen35/cpu.rs:250-259): per
+    token and v-head rms_norm(o) * w * silu(z).  Returns a new array."""
+    o = np.ascontiguousarray(o, np.float32).copy()
+    z = np.ascontiguousarray(z, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    t = o.size // (n_vh * s_dim)
+    lib().orc_delta_back(t, n_vh, s_dim, eps, _f32p(o), _f32p(z), _f32p(w))
+    return o

@@ -37,6 +37,13 @@
  *                        float64 restatement and by invariants (unit RMS,
  *                        norm-preserving pairs, pos 0 and 1e30 factors leave
  *                        the head as normalized).
+ *   orc_delta_front      crates/model/src/qwen35/cpu.rs:193-216 (conv + SiLU,
+ *                        window shift, q/k L2 norm), pinned by a float64
+ *                        restatement and by invariants (identity taps give
+ *                        silu(x); two calls chained equal one call; unit-norm
+ *                        q/k heads).
+ *   orc_delta_back       crates/model/src/qwen35/cpu.rs:250-259 (gated RMS
+ *                        norm), pinned by a float64 restatement.
  *   orc_delta_recur      crates/model/src/qwen35/cpu.rs:218-245 (and the GPU
  *                        form deltanet.wgsl:193-239), pinned by a float64
  *                        matrix restatement and by invariants (exact write at
@@ -436,4 +443,45 @@ void orc_attn_prologue(const orc_prologue *p, float *q, float *k, float *v, cons
     }
     orc_write_cache(p->n_tokens, kv_dim, p->base_pos, p->window, k, k_cache);
     orc_write_cache(p->n_tokens, kv_dim, p->base_pos, p->window, v, v_cache);
+}
+
+/* ------------------------------------------------- delta front and back -- */
+/* ops.rs:175-178 */
+static float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* qwen35/cpu.rs:193-216, per token i in order: channel c of conv_out is
+ * silu(x[i][c]*taps[c][K-1] + sum_{j<K-1} state[j][c]*taps[c][j]), the state
+ * window (K-1 rows, oldest first) then drops its oldest row and appends x[i];
+ * finally each of the 2*key_dim/s_dim q and k heads of conv_out is
+ * L2-normalized (ops.rs:197-203; eps floors the norm). */
+void orc_delta_front(int64_t n_tok, int64_t conv_dim, int64_t key_dim, int64_t s_dim,
+                     int64_t kernel, float eps, const float *x, const float *taps,
+                     float *state, float *conv_out) {
+    for (int64_t i = 0; i < n_tok; ++i) {
+        const float *row = x + i * conv_dim;
+        float *out = conv_out + i * conv_dim;
+        for (int64_t c = 0; c < conv_dim; ++c) {
+            const float *tp = taps + c * kernel;
+            float acc = row[c] * tp[kernel - 1];
+            for (int64_t j = 0; j < kernel - 1; ++j) acc += state[j * conv_dim + c] * tp[j];
+            out[c] = orc_silu(acc);
+        }
+        if (kernel > 1) {
+            memmove(state, state + conv_dim, (size_t)((kernel - 2) * conv_dim) * sizeof(float));
+            memcpy(state + (kernel - 2) * conv_dim, row, (size_t)conv_dim * sizeof(float));
+        }
+        orc_l2_norm_rows(out, 2 * key_dim / s_dim, s_dim, eps);
+    }
+}
+
+/* qwen35/cpu.rs:250-259: per token and v-head, rms_norm_mul(o, w) then
+ * o *= silu(z), in place. */
+void orc_delta_back(int64_t n_tok, int64_t n_vh, int64_t s_dim, float eps, float *o,
+                    const float *z, const float *w) {
+    for (int64_t r = 0; r < n_tok * n_vh; ++r) {
+        float *oh = o + r * s_dim;
+        const float *zh = z + r * s_dim;
+        orc_rms_norm_mul(oh, s_dim, w, eps);
+        for (int64_t j = 0; j < s_dim; ++j) oh[j] *= orc_silu(zh[j]);
+    }
 }

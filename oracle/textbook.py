@@ -181,3 +181,29 @@ def attn_prologue(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, q_stride=
             if v_norm:
                 v[i, h] = rms(v[i, h], None)
     return q.reshape(t, -1), k.reshape(t, -1), v.reshape(t, -1)
+
+
+def delta_front(x, taps, state, *, key_dim, s_dim, eps=1e-6):
+    """Float64 restatement: conv_out[i] = silu(sum_j w[:, j] * [state | x][i + j]),
+    the window's last kernel-1 rows as the new state, q/k heads L2-normalized
+    with the norm floored at eps."""
+    x = np.asarray(x, np.float64)
+    t, conv_dim = x.shape
+    w = np.asarray(taps, np.float64).reshape(conv_dim, -1)
+    kernel = w.shape[1]
+    full = np.concatenate([np.asarray(state, np.float64).reshape(kernel - 1, conv_dim), x], axis=0)
+    acc = np.zeros((t, conv_dim))
+    for j in range(kernel):
+        acc += full[j:j + t] * w[:, j]
+    out = acc / (1.0 + np.exp(-acc))
+    qk = out[:, :2 * key_dim].reshape(t, -1, s_dim)
+    nrm = np.maximum(np.sqrt((qk * qk).sum(-1, keepdims=True)), eps)
+    out[:, :2 * key_dim] = (qk / nrm).reshape(t, -1)
+    return out, full[t:]
+
+
+def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):
+    o = np.asarray(o, np.float64).reshape(-1, n_vh, s_dim)
+    z = np.asarray(z, np.float64).reshape(o.shape)
+    o = o / np.sqrt((o * o).mean(-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+    return (o * (z / (1.0 + np.exp(-z)))).reshape(o.shape[0], -1)

@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 12
+    assert len(names) == 14
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = lmx.lib()
-    assert L.lmx_version() == 101
+    assert L.lmx_version() == 102
     for s in lmx.Status:
         assert L.lmx_status_str(int(s))
     assert L.lmx_status_str(999) == b"unknown status"
@@ -183,3 +183,28 @@ def test_prologue_rejects_bad_pointers_and_dtypes():
     assert _pcall(d, q=FAKE + 2) == lmx.Status.E_ALIGN
     assert _pcall(d, qg=FAKE + 1) == lmx.Status.E_ALIGN
     assert _pcall(d, kc=FAKE + 1) == lmx.Status.E_ALIGN
+
+
+def test_delta_front_back_validation():
+    L = lmx.lib()
+    front = lambda **kw: L.lmx_deltanet_front(
+        ctypes.byref(lmx.DeltaFrontDesc(*[dict(n_tok=4, conv_dim=8192, key_dim=2048, s_dim=128, kernel=4,
+                                               eps=1e-6, **{})[f] if f not in kw else kw[f]
+                                          for f, _ in lmx.DeltaFrontDesc._fields_])),
+        kw.get("x", FAKE), FAKE, FAKE, kw.get("out", FAKE + (1 << 20)), None)
+    assert front(n_tok=0) == lmx.Status.E_SHAPE
+    assert front(conv_dim=8000) == lmx.Status.E_SHAPE
+    assert front(s_dim=96) == lmx.Status.E_UNSUPPORTED
+    assert front(key_dim=5000) == lmx.Status.E_SHAPE
+    assert front(kernel=1) == lmx.Status.E_UNSUPPORTED
+    assert front(kernel=9) == lmx.Status.E_UNSUPPORTED
+    assert front(eps=float("nan")) == lmx.Status.E_SHAPE
+    assert front(x=None) == lmx.Status.E_NULL
+    assert front(x=FAKE + 2) == lmx.Status.E_ALIGN
+    assert front(out=FAKE + 64) == lmx.Status.E_SHAPE  # output overlays the batch
+    back = lambda s_dim=128, n_tok=4, o=FAKE: L.lmx_deltanet_back(
+        ctypes.byref(lmx.DeltaBackDesc(n_tok, 32, s_dim, 1e-6)), o, FAKE, FAKE, None)
+    assert back(s_dim=96) == lmx.Status.E_UNSUPPORTED
+    assert back(n_tok=0) == lmx.Status.E_SHAPE
+    assert back(o=None) == lmx.Status.E_NULL
+    assert back(o=FAKE + 1) == lmx.Status.E_ALIGN

@@ -1,0 +1,94 @@
+"""GPU parity of the delta-net front (lmx_deltanet_front) and back
+(lmx_deltanet_back) against the oracle (qwen35/cpu.rs:193-216, 250-259), and
+the whole delta layer front -> chunked scan -> back against the sequential
+oracle."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import assert_close
+from tests.test_oracle_delta_io import C5, TINY, front_inputs
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import llmoxide_amd as lmx  # noqa: E402
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("shape", [TINY, C5], ids=["tiny", "c5"])
+@pytest.mark.parametrize("t", [1, 2, 3, 5, 64, 65, 300])
+def test_front_matches_oracle(shape, t):
+    say(f"delta front {shape['conv_dim']} t={t}")
+    x, taps, state = front_inputs(shape, t, t)
+    kw = dict(key_dim=shape["key_dim"], s_dim=shape["s_dim"])
+    ref, st_ref = oracle.delta_front(x, taps, state, **kw)
+    sd = dev(state)
+    out = lmx.delta_front(dev(x), dev(taps), sd, **kw)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out")
+    np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)  # the window is copied, bit for bit
+
+
+def test_front_chained_calls_carry_the_window():
+    say("delta front chained")
+    x, taps, state = front_inputs(C5, 70, 4)
+    kw = dict(key_dim=C5["key_dim"], s_dim=C5["s_dim"])
+    ref, st_ref = oracle.delta_front(x, taps, state, **kw)
+    sd, xd, td = dev(state), dev(x), dev(taps)
+    outs = [lmx.delta_front(xd[a:b].contiguous(), td, sd, **kw) for a, b in ((0, 2), (2, 67), (67, 70))]
+    torch.cuda.synchronize()
+    assert_close(torch.cat(outs).cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out")
+    np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)
+
+
+@pytest.mark.parametrize("s_dim", [64, 128, 256])
+def test_back_matches_oracle(s_dim):
+    say(f"delta back s_dim={s_dim}")
+    n_vh, t = 32, 37
+    o = oracle.normal(s_dim + 1, (t, n_vh * s_dim))
+    z = oracle.normal(s_dim + 2, (t, n_vh * s_dim))
+    w = (1.0 + 0.2 * oracle.normal(s_dim + 3, (s_dim,))).astype(np.float32)
+    ref = oracle.delta_back(o, z, w, n_vh=n_vh, s_dim=s_dim)
+    od = dev(o)
+    lmx.delta_back(od, dev(z), dev(w), n_vh=n_vh, s_dim=s_dim)
+    torch.cuda.synchronize()
+    assert_close(od.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="o")
+
+
+def test_delta_layer_front_scan_back_matches_oracle():
+    """C5 delta layer at T=200: front, chunked scan, back on the GPU against the
+    oracle's front, sequential recurrence and back."""
+    say("delta layer front+scan+back")
+    n_vh, n_kh, sd = 32, 16, 128
+    T = 200
+    x, taps, cstate = front_inputs(C5, T, 8)
+    al = oracle.normal(81, (T, n_vh))
+    be = oracle.normal(82, (T, n_vh))
+    z = oracle.normal(83, (T, n_vh * sd))
+    w = (1.0 + 0.2 * oracle.normal(84, (sd,))).astype(np.float32)
+    S0 = (0.1 * oracle.normal(85, (n_vh * sd * sd,))).astype(np.float32)
+    kw = dict(key_dim=C5["key_dim"], s_dim=sd)
+    conv, _ = oracle.delta_front(x, taps, cstate, **kw)
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    y_ref = oracle.delta_back(o_ref, z, w, n_vh=n_vh, s_dim=sd)
+
+    A = dev(np.full(n_vh, -1.0, np.float32))
+    dt = dev(np.zeros(n_vh, np.float32))
+    state = dev(S0.copy())
+    conv_d = lmx.delta_front(dev(x), dev(taps), dev(cstate), **kw)
+    o = lmx.delta_chunked(conv_d, dev(al), dev(be), state, A, dt, n_vh=n_vh, n_kh=n_kh, s_dim=sd, chunk=64)
+    lmx.delta_back(o, dev(z), dev(w), n_vh=n_vh, s_dim=sd)
+    torch.cuda.synchronize()
+    assert_close(o.cpu().numpy(), y_ref, what="layer output")
+    assert_close(state.cpu().numpy(), S_ref, what="S")

@@ -1,0 +1,74 @@
+"""Oracle for the delta-net front (causal conv + SiLU, window shift, q/k L2
+norm; qwen35/cpu.rs:193-216) and back (gated RMS norm; qwen35/cpu.rs:250-259):
+a float64 restatement, invariants and a planted mistake.  Test infrastructure only."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import textbook
+
+C5 = dict(conv_dim=8192, key_dim=2048, s_dim=128, kernel=4)
+TINY = dict(conv_dim=256, key_dim=64, s_dim=64, kernel=4)
+
+
+def front_inputs(shape, t, seed):
+    cd, k = shape["conv_dim"], shape["kernel"]
+    x = oracle.normal(seed * 10 + 1, (t, cd))
+    taps = (0.5 * oracle.normal(seed * 10 + 2, (cd, k))).astype(np.float32)
+    state = oracle.normal(seed * 10 + 3, (k - 1, cd))
+    return x, taps, state
+
+
+@pytest.mark.parametrize("shape", [TINY, C5], ids=["tiny", "c5"])
+@pytest.mark.parametrize("t", [1, 2, 3, 17])
+def test_front_matches_float64(shape, t):
+    x, taps, state = front_inputs(shape, t, t)
+    kw = dict(key_dim=shape["key_dim"], s_dim=shape["s_dim"])
+    out, st = oracle.delta_front(x, taps, state, **kw)
+    ref, st_ref = textbook.delta_front(x, taps, state, **kw)
+    np.testing.assert_allclose(out, ref, rtol=0, atol=2e-6)
+    np.testing.assert_array_equal(st, st_ref.astype(np.float32))
+
+
+def test_front_identity_taps_give_silu_then_norm():
+    x, taps, state = front_inputs(TINY, 5, 1)
+    taps = np.zeros_like(taps)
+    taps[:, -1] = 1.0  # only the current row
+    out, _ = oracle.delta_front(x, taps, state, key_dim=TINY["key_dim"], s_dim=TINY["s_dim"])
+    silu = x / (1.0 + np.exp(-x.astype(np.float64)))
+    np.testing.assert_allclose(out[:, 2 * TINY["key_dim"]:], silu[:, 2 * TINY["key_dim"]:], atol=1e-6)
+    qk = out[:, :2 * TINY["key_dim"]].reshape(5, -1, TINY["s_dim"]).astype(np.float64)
+    np.testing.assert_allclose(np.sqrt((qk * qk).sum(-1)), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 6])
+def test_front_two_calls_equal_one(split):
+    """The conv window carries the state across calls: a batch cut in two
+    gives the same output and final window as the whole batch."""
+    x, taps, state = front_inputs(TINY, 9, 2)
+    kw = dict(key_dim=TINY["key_dim"], s_dim=TINY["s_dim"])
+    whole, st_whole = oracle.delta_front(x, taps, state, **kw)
+    a, st_a = oracle.delta_front(x[:split], taps, state, **kw)
+    b, st_b = oracle.delta_front(x[split:], taps, st_a, **kw)
+    np.testing.assert_array_equal(np.concatenate([a, b]), whole)
+    np.testing.assert_array_equal(st_b, st_whole)
+
+
+def test_planted_window_order_mistake_is_detected():
+    """Reading the window newest-first (a plausible index slip) changes the output."""
+    x, taps, state = front_inputs(TINY, 3, 3)
+    kw = dict(key_dim=TINY["key_dim"], s_dim=TINY["s_dim"])
+    out, _ = oracle.delta_front(x, taps, state, **kw)
+    wrong, _ = textbook.delta_front(x, taps[:, [2, 1, 0, 3]], state, **kw)
+    assert np.abs(out - wrong).max() > 1e-3
+
+
+@pytest.mark.parametrize("s_dim", [64, 128, 256])
+def test_back_matches_float64(s_dim):
+    n_vh, t = 4, 6
+    o = oracle.normal(s_dim + 1, (t, n_vh * s_dim))
+    z = oracle.normal(s_dim + 2, (t, n_vh * s_dim))
+    w = (1.0 + 0.2 * oracle.normal(s_dim + 3, (s_dim,))).astype(np.float32)
+    got = oracle.delta_back(o, z, w, n_vh=n_vh, s_dim=s_dim)
+    ref = textbook.delta_back(o, z, w, n_vh=n_vh, s_dim=s_dim)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=2e-6 * float(np.abs(ref).max()))
