@@ -39,6 +39,19 @@ __device__ __forceinline__ float row_sum16(float x) {
     return x;
 }
 
+// Sum over the 64 lanes of a wave (all lanes active); every lane gets the
+// total.  Four DPP steps per row, then the four row totals through SGPRs:
+// no LDS round trip, unlike a ds_bpermute butterfly.
+__device__ __forceinline__ float wave_sum64(float x) {
+    x = row_sum16(x);
+    const int b = __builtin_bit_cast(int, x);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float shfl_xor(float x, int m) { return __shfl_xor(x, m, 64); }
 
 // Load N consecutive f16 values (N a multiple of 4) as floats.

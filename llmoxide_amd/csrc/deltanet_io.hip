@@ -7,11 +7,12 @@
 // round trip through HBM before the norm, and the window update goes through
 // a scratch copy so that no thread reads a row another one is overwriting.
 // Here one workgroup owns a 128-channel block (one q/k head at s_dim 128)
-// for a chunk of tokens: its waves take the chunk's tokens in turn, a lane
-// holds two channels (lane and lane + 64), the conv reads its K-1 earlier
-// rows from the batch (or, before the batch, from the window) in the
-// reference's order, and the head's L2 norm is a wave reduction, so each
-// output row is written once.  Only the first chunk's workgroup of a block
+// for a chunk of 64 tokens: each wave takes 16 consecutive tokens, a lane
+// holds two channels (lane and lane + 64), the K-1 rows before the wave's
+// tokens (from the batch, or before it from the window) and its own rows are
+// loaded once into registers, the taps slide over them in the reference's
+// order, and the head's L2 norm is a wave reduction, so each output row is
+// written once.  Only the first chunk's workgroup of a block
 // reads the old window, so it alone writes the new one, after its own reads:
 // no workgroup ever reads a window row another one writes.
 //
@@ -24,12 +25,6 @@ namespace lmx {
 constexpr int kFrontTokens = 64;  // tokens per front workgroup (>= kernel - 1)
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
-
-__device__ __forceinline__ float wave_sum64(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-    return x;
-}
 
 struct FrontArgs {
     const float* x;
@@ -53,37 +48,54 @@ __global__ __launch_bounds__(256) void delta_front_kernel(FrontArgs a) {
         t0[j] = a.taps[(size_t)c0 * K + j];
         t1[j] = a.taps[(size_t)c1 * K + j];
     }
-    const int tok_end = min(a.n_tok, (tc + 1) * kFrontTokens);
-    for (int tok = tc * kFrontTokens + w; tok < tok_end; tok += 4) {
-        const float* xr = a.x + (size_t)tok * a.conv_dim;
-        // qwen35/cpu.rs:200-204: the current row's term first, then the
-        // window rows oldest first
-        float acc0 = xr[c0] * t0[K - 1], acc1 = xr[c1] * t1[K - 1];
+    // Wave w takes tokens [tok0, tok0 + 16) of the chunk: the K-1 rows before
+    // tok0 and its 16 rows are loaded once, into registers, and the taps slide
+    // over them (each batch row is read once per wave, not K times).
+    constexpr int NT = kFrontTokens / 4;
+    const int tok0 = tc * kFrontTokens + NT * w;
+    const int nt = min(NT, a.n_tok - tok0);
+    if (nt > 0) {  // uniform per wave
+        float r0[NT + K - 1], r1[NT + K - 1];
 #pragma unroll
-        for (int j = 0; j < K - 1; ++j) {
-            const int p = tok + j - (K - 1);
-            const float* row = p >= 0 ? a.x + (size_t)p * a.conv_dim
-                                      : a.state + (size_t)(p + K - 1) * a.conv_dim;
-            acc0 += row[c0] * t0[j];
-            acc1 += row[c1] * t1[j];
-        }
-        float y0 = silu_f(acc0), y1 = silu_f(acc1);
-        if (qk) {
-            // ops.rs:197-203: x / max(||x||, eps) per head
-            if (a.s_dim == 128) {
-                const float sc = 1.f / fmaxf(sqrtf(wave_sum64(y0 * y0 + y1 * y1)), a.eps);
-                y0 *= sc;
-                y1 *= sc;
-            } else {  // s_dim 64: lane holds one channel of each of two heads
-                const float s0 = 1.f / fmaxf(sqrtf(wave_sum64(y0 * y0)), a.eps);
-                const float s1 = 1.f / fmaxf(sqrtf(wave_sum64(y1 * y1)), a.eps);
-                y0 *= s0;
-                y1 *= s1;
+        for (int idx = 0; idx < NT + K - 1; ++idx) {
+            const int p = tok0 - (K - 1) + idx;
+            r0[idx] = r1[idx] = 0.f;
+            if (p < a.n_tok) {  // uniform
+                const float* row = p >= 0 ? a.x + (size_t)p * a.conv_dim
+                                          : a.state + (size_t)(p + K - 1) * a.conv_dim;
+                r0[idx] = row[c0];
+                r1[idx] = row[c1];
             }
         }
-        float* orow = a.out + (size_t)tok * a.conv_dim;
-        orow[c0] = y0;
-        orow[c1] = y1;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            if (i >= nt) continue;  // uniform
+            // qwen35/cpu.rs:200-204: the current row's term first, then the
+            // window rows oldest first
+            float acc0 = r0[i + K - 1] * t0[K - 1], acc1 = r1[i + K - 1] * t1[K - 1];
+#pragma unroll
+            for (int j = 0; j < K - 1; ++j) {
+                acc0 += r0[i + j] * t0[j];
+                acc1 += r1[i + j] * t1[j];
+            }
+            float y0 = silu_f(acc0), y1 = silu_f(acc1);
+            if (qk) {
+                // ops.rs:197-203: x / max(||x||, eps) per head
+                if (a.s_dim == 128) {
+                    const float sc = 1.f / fmaxf(sqrtf(wave_sum64(y0 * y0 + y1 * y1)), a.eps);
+                    y0 *= sc;
+                    y1 *= sc;
+                } else {  // s_dim 64: lane holds one channel of each of two heads
+                    const float s0 = 1.f / fmaxf(sqrtf(wave_sum64(y0 * y0)), a.eps);
+                    const float s1 = 1.f / fmaxf(sqrtf(wave_sum64(y1 * y1)), a.eps);
+                    y0 *= s0;
+                    y1 *= s1;
+                }
+            }
+            float* orow = a.out + (size_t)(tok0 + i) * a.conv_dim;
+            orow[c0] = y0;
+            orow[c1] = y1;
+        }
     }
 
     // The window after the batch: row r of the new state is position

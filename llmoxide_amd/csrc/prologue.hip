@@ -8,14 +8,19 @@
 // the activations.  Here one workgroup owns one token: it builds the token's
 // cos/sin table once (the angle depends on the position and the pair, not on
 // the head), then its four waves take the token's Q, K and V head rows in
-// turn.  A row is read once, normalized in registers (wave reduction),
-// staged in the wave's LDS slot for the pair exchange of the rotation, and
-// written once: Q back in place as f32, K and V straight into the f16 caches.
+// turn.  A row is read once, normalized in registers (DPP wave reduction),
+// rotated with its pair partner taken from the same lane, a neighbour lane
+// or LDS depending on n_rot, and written once: Q back in place as f32, K and
+// V straight into the f16 caches.
 //
-// Angles follow ops.rs:142-159 exactly: theta starts at pos and is multiplied
-// by base^(-2/n_rot) once per pair in double (the host passes the factor from
-// the same libm pow), the pair's factor divides it in double, and sin / cos
-// are rounded to float.
+// Angles follow ops.rs:142-159 in double: pair i's angle is pos * s^i with
+// s = base^(-2/n_rot) from the same libm pow, divided by the pair's factor,
+// and sin / cos are rounded to float.  The reference forms s^i by i
+// successive products, this kernel by the bits of i (at most 8 products from
+// s^(2^k) the host squares out), so the doubles agree to a few ulps
+// (relative 1e-15, i.e. 3e-11 rad at position 32k) and the float sin / cos
+// agree unless that lands on a float rounding boundary.  The RMS scale is
+// v_rsq_f32 (1 ulp).
 #include <cmath>
 
 #include "common.hpp"
@@ -33,111 +38,161 @@ struct PrologueArgs {
     f16* v_cache;
     int n_tokens, H, Hkv, hd, q_stride, n_rot, base_pos, window, v_norm;
     float eps;
-    double theta_scale;
+    double scale_pow[8];  // s^(2^k), s = base^(-2/n_rot): pair i's angle is pos * s^i
 };
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-    return x;
-}
 
 // NJ = head_dim / 64: lane l holds dims l + 64 j of a row.
 template <int NJ>
 __global__ __launch_bounds__(256) void attn_prologue_kernel(PrologueArgs a) {
     constexpr int HD = 64 * NJ;
+    constexpr int RB = 32 / NJ;  // rows of one batch held in registers (32 VGPRs)
     __shared__ float cs_tab[HD / 2], sn_tab[HD / 2];
     __shared__ float row_s[4][HD];
     const int tok = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int pos = a.base_pos + tok;
     const int half = a.n_rot / 2;
-
-    for (int i = tid; i < half; i += 256) {
-        double theta = (double)pos;
-        for (int j = 0; j < i; ++j) theta *= a.theta_scale;
-        const double ang = theta / (a.factors ? (double)a.factors[i] : 1.0);
-        cs_tab[i] = (float)cos(ang);
-        sn_tab[i] = (float)sin(ang);
-    }
-    __syncthreads();
-
     const int kv_dim = a.Hkv * HD;
     // With a ring, a later token of this call that maps to the same slot
     // overwrites this one (the reference stores rows in order): skip it.
     const bool store = !a.window || tok + a.window >= a.n_tokens;
     const size_t slot = a.window ? (size_t)(pos % a.window) : (size_t)pos;
     const int n_rows = a.H + 2 * a.Hkv;
-    for (int r = w; r < n_rows; r += 4) {
-        const float* src;
-        const float* gain = nullptr;
-        bool norm, rot;
-        float* dst32 = nullptr;
-        f16* dst16 = nullptr;
-        if (r < a.H) {
-            dst32 = a.q + ((size_t)tok * a.H + r) * a.q_stride;
-            src = dst32;
-            gain = a.q_gain;
-            norm = gain != nullptr;
-            rot = true;
-        } else if (r < a.H + a.Hkv) {
-            const int h = r - a.H;
-            src = a.k + (size_t)tok * kv_dim + h * HD;
-            gain = a.k_gain;
-            norm = gain != nullptr;
-            rot = true;
-            dst16 = a.k_cache + slot * kv_dim + h * HD;
-        } else {
-            const int h = r - a.H - a.Hkv;
-            src = a.v + (size_t)tok * kv_dim + h * HD;
-            norm = a.v_norm != 0;
-            rot = false;
-            dst16 = a.v_cache + slot * kv_dim + h * HD;
-        }
-        if (!dst32 && !store) continue;  // uniform per wave
+    // Row r of this token: query head r, K head r - H, or V head r - H - Hkv.
+    auto row_src = [&](int r) -> const float* {
+        if (r < a.H) return a.q + ((size_t)tok * a.H + r) * a.q_stride;
+        if (r < a.H + a.Hkv) return a.k + (size_t)tok * kv_dim + (r - a.H) * HD;
+        return a.v + (size_t)tok * kv_dim + (r - a.H - a.Hkv) * HD;
+    };
 
-        float x[NJ];
+    // Everything this wave reads is requested up front: the gains, then its
+    // rows w, w + 4, ... (a batch of up to RB), and the loads are in flight
+    // while the angle table is built.  On gfx9 a store and a later load share
+    // one counter, so waiting on a load issued after a store waits for the
+    // store too; here each batch waits once, before its first store.
+    float qg[NJ], kg[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) x[j] = src[lane + 64 * j];
-        if (norm) {
-            // ops.rs:40-47: x / sqrt(mean(x^2) + eps), then the gain
-            float ss = 0.f;
+    for (int j = 0; j < NJ; ++j) qg[j] = kg[j] = 1.f;
+    if (a.q_gain)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) ss += x[j] * x[j];
-            const float sc = 1.f / sqrtf(wave_sum(ss) / (float)HD + a.eps);
+        for (int j = 0; j < NJ; ++j) qg[j] = a.q_gain[lane + 64 * j];
+    if (a.k_gain)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) x[j] *= sc;
-            if (gain)
+        for (int j = 0; j < NJ; ++j) kg[j] = a.k_gain[lane + 64 * j];
+    float xb[RB][NJ];
+    auto load_batch = [&](int r0) {
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) x[j] *= gain[lane + 64 * j];
-        }
-        if (rot && half > 0) {
+        for (int b = 0; b < RB; ++b) {
+            const int r = r0 + 4 * b;
+            if (r < n_rows && (r < a.H || store)) {  // uniform per wave
+                const float* src = row_src(r);
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) row_s[w][lane + 64 * j] = x[j];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int d = lane + 64 * j;
-                if (d < half) {
-                    x[j] = row_s[w][d] * cs_tab[d] - row_s[w][d + half] * sn_tab[d];
-                } else if (d < a.n_rot) {
-                    const int i = d - half;
-                    x[j] = row_s[w][i] * sn_tab[i] + row_s[w][d] * cs_tab[i];
-                }
+                for (int j = 0; j < NJ; ++j) xb[b][j] = src[lane + 64 * j];
             }
-            // the slot is rewritten by this wave's next row only after these reads
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        if (dst32) {
+    };
+    load_batch(w);
+
+    for (int i = tid; i < half; i += 256) {
+        double theta = (double)pos;  // pos * s^i by the bits of i (i < 256)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) dst32[lane + 64 * j] = x[j];
-        } else {
+        for (int k = 0; k < 8; ++k) theta *= (i >> k) & 1 ? a.scale_pow[k] : 1.0;
+        double ang = theta;
+        if (a.factors) ang = theta / (double)a.factors[i];  // the load is waited on here only
+        double s, c;
+        sincos(ang, &s, &c);
+        cs_tab[i] = (float)c;
+        sn_tab[i] = (float)s;
+    }
+    __syncthreads();
+
+    // Rotation of dim d with its partner p (d + half below half, d - half
+    // above): out = x cos + p sin', with sin' = -sin below half.  The partner
+    // sits in the same lane when half is a multiple of 64, in lane
+    // d +- half of register 0 when n_rot <= 64, else it goes through LDS.
+    const int mode = half == 0 ? 0 : (half % 64 == 0 ? 1 : (a.n_rot <= 64 ? 2 : 3));
+    const int hj = half / 64;
+    float cr[NJ], sr[NJ];
+    bool rj[NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) dst16[lane + 64 * j] = (f16)x[j];
+    for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        rj[j] = d < a.n_rot;
+        const int i = d < half ? d : d - half;
+        cr[j] = rj[j] ? cs_tab[i] : 1.f;
+        sr[j] = rj[j] ? (d < half ? -sn_tab[i] : sn_tab[i]) : 0.f;
+    }
+    const int xlane = lane < half ? lane + half : lane - half;
+
+    for (int r0 = w; r0 < n_rows; r0 += 4 * RB) {
+        if (r0 != w) load_batch(r0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the batch is in registers
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const int r = r0 + 4 * b;
+            if (r >= n_rows) continue;  // uniform per wave
+            const bool is_q = r < a.H, is_k = !is_q && r < a.H + a.Hkv;
+            if (!is_q && !store) continue;  // uniform per wave
+            const bool has_gain = is_q ? a.q_gain != nullptr : (is_k && a.k_gain != nullptr);
+            const bool norm = (is_q || is_k) ? has_gain : a.v_norm != 0;
+            float* x = xb[b];
+            if (norm) {
+                // ops.rs:40-47: x / sqrt(mean(x^2) + eps), then the gain
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) ss += x[j] * x[j];
+                const float sc = __builtin_amdgcn_rsqf(wave_sum64(ss) / (float)HD + a.eps);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) x[j] *= sc;
+                if (has_gain)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) x[j] *= is_q ? qg[j] : kg[j];
+            }
+            if ((is_q || is_k) && mode != 0) {
+                float p[NJ];
+                if (mode == 1) {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        p[j] = 0.f;
+#pragma unroll
+                        for (int j2 = 0; j2 < NJ; ++j2) {
+                            if (j < hj && j2 == j + hj) p[j] = x[j2];
+                            if (j >= hj && j < 2 * hj && j2 + hj == j) p[j] = x[j2];
+                        }
+                    }
+                } else if (mode == 2) {
+                    p[0] = __shfl(x[0], xlane, 64);
+#pragma unroll
+                    for (int j = 1; j < NJ; ++j) p[j] = 0.f;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) row_s[w][lane + 64 * j] = x[j];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int d = lane + 64 * j;
+                        p[j] = rj[j] ? row_s[w][d < half ? d + half : d - half] : 0.f;
+                    }
+                    // the slot is rewritten by this wave's next row only after these reads
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) x[j] = rj[j] ? x[j] * cr[j] + p[j] * sr[j] : x[j];
+            }
+            if (is_q) {
+                float* dst = a.q + ((size_t)tok * a.H + r) * a.q_stride;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) dst[lane + 64 * j] = x[j];
+            } else {
+                f16* dst = (is_k ? a.k_cache + (r - a.H) * HD : a.v_cache + (r - a.H - a.Hkv) * HD) +
+                           slot * kv_dim;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) dst[lane + 64 * j] = (f16)x[j];
+            }
         }
     }
 }
@@ -166,7 +221,8 @@ lmx_status attn_prologue(const lmx_prologue_desc* d, float* q, const float* k_ne
     a.v_norm = (int)d->v_norm;
     a.eps = d->rms_eps;
     // ops.rs:145: (base as f64).powf(-2.0 / d as f64), d = the rotated length
-    a.theta_scale = d->n_rot ? std::pow((double)d->rope_base, -2.0 / (double)d->n_rot) : 1.0;
+    double s = d->n_rot ? std::pow((double)d->rope_base, -2.0 / (double)d->n_rot) : 1.0;
+    for (int k = 0; k < 8; ++k, s *= s) a.scale_pow[k] = s;
     (void)hipGetLastError();
     const dim3 grid(d->n_tokens);
     switch (d->head_dim) {

@@ -81,3 +81,10 @@ def test_prologue_prefill_batch():
 
 def test_prologue_without_norms_is_rope_and_store_only():
     run("qwen3", t=5, base_pos=11, overrides=dict(q_gain=None, k_gain=None))
+
+
+@pytest.mark.parametrize("n_rot", [0, 32, 96])
+def test_prologue_partial_rotation_widths(n_rot):
+    # n_rot 32 pairs lanes within one register, 96 pairs across registers at a
+    # lane offset (the LDS exchange), 0 rotates nothing
+    run("qwen3", t=6, base_pos=1000, overrides=dict(n_rot=n_rot))

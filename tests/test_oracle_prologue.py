@@ -17,6 +17,9 @@ CONFIGS = {
                       v_norm=True, window=16),
     "gemma_global": dict(n_heads=4, n_kv_heads=1, head_dim=256, n_rot=256, rope_base=1e6, q_stride=256,
                          v_norm=True, factors=True),
+    # the smallest and largest head sizes the path takes, with partial rope on the latter
+    "hd64": dict(n_heads=4, n_kv_heads=2, head_dim=64, n_rot=64, rope_base=1e4, q_stride=64),
+    "hd512_partial": dict(n_heads=2, n_kv_heads=1, head_dim=512, n_rot=128, rope_base=1e6, q_stride=512),
 }
 
 
