@@ -129,7 +129,9 @@ lmx_status lmx_kv_append(const lmx_kv_desc *d, const float *k_new, const float *
  *   slot(pos); the latest position wins a ring slot).
  * rope_neox pairs dims (j, j + n_rot/2) with angle
  *   pos * rope_base^(-2j/n_rot) / factor_j  (factor_j = rope_factors[j], or 1
- *   when rope_factors is NULL), accumulated in double as the reference does.
+ *   when rope_factors is NULL), in double; the reference multiplies j times
+ *   by rope_base^(-2/n_rot), this library by the bits of j, which agree to a
+ *   few double ulps before sin/cos are rounded to float.
  * head_dim: 64, 128, 256 or 512; n_rot even, <= head_dim; q_stride >= head_dim.
  * k_new/v_new are read only. */
 typedef struct {
