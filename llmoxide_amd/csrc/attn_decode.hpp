@@ -9,13 +9,19 @@
 //
 // Work split.  A workgroup owns HW kv heads (one wave group per head) for a
 // block of GB query heads per kv head, one query row, and split s of the
-// visible keys: the contiguous 16-key tiles [s*tps, (s+1)*tps).  With HW = 8
-// and one wave per head, the workgroup's loads cover whole cache rows (a
-// row holds every kv head), which is the access pattern HBM serves fastest;
-// K/V rows are read once for all GB query heads of a kv head (GQA) and with
+// visible keys: the contiguous 16-key tiles [s*tps, (s+1)*tps).  K/V rows
+// are read once for all GB query heads of a kv head (GQA) and with
 // non-temporal loads (they are streamed, never re-read).  Each wave keeps
-// two tiles of K/V in registers: while it computes one, the next one's loads
-// are in flight.  Row addressing is branch-free: a linear cache reads row p,
+// DEPTH tiles of K/V in registers: while it computes one, the next ones'
+// loads are in flight.
+//
+// A workgroup is four waves, one per SIMD.  When two streaming waves share
+// a SIMD, the memory pipeline serves the first one faster (measured with
+// eight-wave workgroups at H 32, Hkv 8, hd 128 over 32k keys: the first wave
+// of each SIMD finished its equal share at 16 us, the second at 22 us, and
+// giving the first more of the tiles only slowed it without speeding the
+// second).  With one wave
+// per SIMD and one workgroup per CU nobody waits on a slower partner.  Row addressing is branch-free: a linear cache reads row p,
 // a ring reads slot p % window (multiply-high division), and rows of the
 // current batch can come from a separate k_cur/v_cur buffer.
 //
@@ -73,7 +79,7 @@ struct DecodeArgs {
     float c;                // scale * log2(e)
 };
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;  // one wave per SIMD (see "Work split")
 constexpr int kDecThreads = kWaves * 64;
 constexpr int kMaxP = 512;  // splits per unit
 constexpr int kTile = 16;   // keys per wave tile
@@ -241,10 +247,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
     constexpr bool PIPE = HD <= 128;
-    // Tiles in flight per wave: as many as the register file allows at two
-    // waves per SIMD (a 16-key tile is 16 K + 16 V registers per lane at
-    // hd 128, 8 + 8 at hd 64).
-    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : (GB <= 4 ? 3 : 2));
+    // Tiles in flight per wave (a 16-key tile is 16 K + 16 V registers per
+    // lane at hd 128, 8 + 8 at hd 64).  At hd 128 two measured best: with
+    // one wave per SIMD, deeper buffers (3, 4, 6) only lengthen the start.
+    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : 2);
     static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
     static_assert(VR * VW == DPL, "V lane layout");
     static_assert(kWaves % HW == 0, "waves per head");
@@ -598,7 +604,6 @@ template <typename QT, int MODE>
 inline lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, int hw, dim3 grid,
                                 hipStream_t st) {
     switch (hw) {
-        case 8: return launch_decode_hw<QT, MODE, 8>(a, hd, gb, grid, st);
         case 4: return launch_decode_hw<QT, MODE, 4>(a, hd, gb, grid, st);
         case 2: return launch_decode_hw<QT, MODE, 2>(a, hd, gb, grid, st);
         default: return launch_decode_hw<QT, MODE, 1>(a, hd, gb, grid, st);
