@@ -339,6 +339,43 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     __shared__ __attribute__((aligned(16))) float P_s[kWaves][kTile][8];
     __shared__ __attribute__((aligned(16))) float C_s[kWaves][4][8];
 
+    // Combine the WPH waves of each head slot (after a workgroup barrier):
+    // element (hs, g, d) of the workgroup; waves hs, hs + HW, ... hold its
+    // parts.
+    auto combine_waves = [&]() {
+      if constexpr (WPH > 1) {  // never instantiated with one wave per head
+        __syncthreads();
+        for (int idx = tid; idx < HW * GB * HD; idx += kDecThreads) {
+            const int e_hs = idx / (GB * HD);
+            const int rem = idx - e_hs * (GB * HD);
+            const int g = rem / HD, d = rem - g * HD;
+            float Mw = sm_m[e_hs][g];
+#pragma unroll
+            for (int ww = 1; ww < WPH; ++ww) Mw = fmaxf(Mw, sm_m[e_hs + ww * HW][g]);
+            float O = 0.f, Lw = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < WPH; ++ww) {
+                const int w = e_hs + ww * HW;
+                const float sc = fast_exp2(sm_m[w][g] - Mw);
+                O = fmaf(sm_o[w][g][d], sc, O);
+                Lw = fmaf(sm_l[w][g], sc, Lw);
+            }
+            const int head = (kvg * HW + e_hs) * a.G + hb * GB + g;
+            const size_t row = (size_t)qi * a.H + head;
+            if (p_u == 1) {
+                a.out[row * HD + d] = O / Lw;
+            } else {
+                const size_t pidx = row * a.P + split;
+                a.part_o[pidx * HD + d] = O;
+                if (d == 0) {
+                    a.part_ml[pidx * 2] = Mw;
+                    a.part_ml[pidx * 2 + 1] = Lw;
+                }
+            }
+        }
+      }
+    };
+
     // Everything from the first load to the wave's partial sits in one
     // uniform branch: no path merges loads issued with loads not issued, so
     // the compiler's wait counts stay exact.
@@ -511,67 +548,91 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         L += shfl_xor(L, 32);
         if (c16 < GB) C_s[wave][g4][c16] = gsc;
         wave_lds_sync();
+        if constexpr (WPH == 1) {
+            // The wave is its head's only one here: a reduce-scatter through
+            // LDS (each group writes its weighted o, then lane (g4, c16)
+            // sums head g4's dims over the four groups) and the wave stores
+            // its result itself, with no workgroup barrier.
+            __shared__ __attribute__((aligned(16))) float red_s[kWaves][4][GB][HD];
+            __shared__ float lsum_s[kWaves][GB];
 #pragma unroll
-        for (int h = 0; h < GB; ++h) {
-            const float sc = C_s[wave][g4][h];
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                float x = o[h][d] * sc;
-                x += shfl_xor(x, 16);
-                x += shfl_xor(x, 32);
-                o[h][d] = x;
-            }
-        }
-        if (g4 == 0) {
-#pragma unroll
-            for (int h = 0; h < GB; ++h)
+            for (int h = 0; h < GB; ++h) {
+                const float sc = C_s[wave][g4][h];
 #pragma unroll
                 for (int r = 0; r < VR; ++r)
 #pragma unroll
-                    for (int j = 0; j < VW; ++j) sm_o[wave][h][v_dim<HD>(c16, r, j)] = o[h][VW * r + j];
-            if (c16 < GB) {
-                sm_m[wave][c16] = M;
-                sm_l[wave][c16] = L;
+                    for (int j = 0; j < VW; ++j)
+                        red_s[wave][g4][h][v_dim<HD>(c16, r, j)] = o[h][VW * r + j] * sc;
             }
-        }
-    } else if (c16 < GB && g4 == 0) {
-        // A wave without tiles contributes nothing: weight exp2(-1e30 - M) = 0.
-        sm_m[wave][c16] = -1e30f;
-        sm_l[wave][c16] = 0.f;
-        for (int d = 0; d < HD; ++d) sm_o[wave][c16][d] = 0.f;
-    }
-    __syncthreads();
-
-    // Combine the WPH waves of each head slot: element (hs, g, d) of the
-    // workgroup; waves hs, hs + HW, ... hold its parts.
-    for (int idx = tid; idx < HW * GB * HD; idx += kDecThreads) {
-        const int e_hs = idx / (GB * HD);
-        const int rem = idx - e_hs * (GB * HD);
-        const int g = rem / HD, d = rem - g * HD;
-        float Mw = sm_m[e_hs][g];
+            if (c16 < GB && g4 == 0) lsum_s[wave][c16] = L;
+            wave_lds_sync();
 #pragma unroll
-        for (int ww = 1; ww < WPH; ++ww) Mw = fmaxf(Mw, sm_m[e_hs + ww * HW][g]);
-        float O = 0.f, Lw = 0.f;
+            for (int h0g = 0; h0g < GB; h0g += 4) {
+                const int h = h0g + g4;
+                if (h < GB) {
+                    const size_t row = (size_t)qi * a.H + h0 + h;
+                    const float inv = 1.f / lsum_s[wave][h];
 #pragma unroll
-        for (int ww = 0; ww < WPH; ++ww) {
-            const int w = e_hs + ww * HW;
-            const float sc = fast_exp2(sm_m[w][g] - Mw);
-            O = fmaf(sm_o[w][g][d], sc, O);
-            Lw = fmaf(sm_l[w][g], sc, Lw);
-        }
-        const int head = (kvg * HW + e_hs) * a.G + hb * GB + g;
-        const size_t row = (size_t)qi * a.H + head;
-        if (p_u == 1) {
-            a.out[row * HD + d] = O / Lw;
+                    for (int r = 0; r < VR; ++r) {
+                        const int d0 = v_dim<HD>(c16, r, 0);
+                        float acc[VW];
+#pragma unroll
+                        for (int j = 0; j < VW; ++j) acc[j] = red_s[wave][0][h][d0 + j];
+#pragma unroll
+                        for (int g = 1; g < 4; ++g)
+#pragma unroll
+                            for (int j = 0; j < VW; ++j) acc[j] += red_s[wave][g][h][d0 + j];
+                        float* dst = p_u == 1 ? a.out + row * HD + d0
+                                              : a.part_o + (row * a.P + split) * HD + d0;
+#pragma unroll
+                        for (int j = 0; j < VW; j += 4)
+                            *reinterpret_cast<f32x4*>(dst + j) =
+                                p_u == 1 ? f32x4{acc[j] * inv, acc[j + 1] * inv, acc[j + 2] * inv,
+                                                 acc[j + 3] * inv}
+                                         : f32x4{acc[j], acc[j + 1], acc[j + 2], acc[j + 3]};
+                    }
+                }
+            }
+            if (p_u > 1 && g4 == 0 && c16 < GB) {
+                const size_t pidx = ((size_t)qi * a.H + h0 + c16) * a.P + split;
+                a.part_ml[pidx * 2] = M;
+                a.part_ml[pidx * 2 + 1] = L;
+            }
         } else {
-            const size_t pidx = row * a.P + split;
-            a.part_o[pidx * HD + d] = O;
-            if (d == 0) {
-                a.part_ml[pidx * 2] = Mw;
-                a.part_ml[pidx * 2 + 1] = Lw;
+#pragma unroll
+            for (int h = 0; h < GB; ++h) {
+                const float sc = C_s[wave][g4][h];
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) {
+                    float x = o[h][d] * sc;
+                    x += shfl_xor(x, 16);
+                    x += shfl_xor(x, 32);
+                    o[h][d] = x;
+                }
+            }
+            if (g4 == 0) {
+#pragma unroll
+                for (int h = 0; h < GB; ++h)
+#pragma unroll
+                    for (int r = 0; r < VR; ++r)
+#pragma unroll
+                        for (int j = 0; j < VW; ++j) sm_o[wave][h][v_dim<HD>(c16, r, j)] = o[h][VW * r + j];
+                if (c16 < GB) {
+                    sm_m[wave][c16] = M;
+                    sm_l[wave][c16] = L;
+                }
             }
         }
+    } else if constexpr (WPH > 1) {
+        // A wave without tiles contributes nothing: weight exp2(-1e30 - M) = 0.
+        // (With one wave per head every wave has a tile: t_begin < n_tiles.)
+        if (c16 < GB && g4 == 0) {
+            sm_m[wave][c16] = -1e30f;
+            sm_l[wave][c16] = 0.f;
+            for (int d = 0; d < HD; ++d) sm_o[wave][c16][d] = 0.f;
+        }
     }
+    if constexpr (WPH > 1) combine_waves();
 }
 
 struct DecodePlan {
