@@ -78,7 +78,7 @@ typedef struct {
 
 /* The delta-net uniform, deltanet.wgsl:20-34 / qwen35.rs:51-68, restricted to
  * what the recurrence reads.  Conv taps and the conv window belong to the
- * prologue kernels, which stay outside this library. */
+ * delta-net front (lmx_deltanet_front, below). */
 typedef struct {
     uint32_t n_tok;       /* tokens in the batch                              */
     uint32_t conv_dim;    /* row stride of the conv stream, 2*key_dim+d_inner */
@@ -179,6 +179,37 @@ lmx_status lmx_attn_fwd(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,
                         const void *k_cache, const void *v_cache, lmx_dtype kv_dt,
                         const void *k_cur, const void *v_cur, float *out,
                         void *ws, size_t ws_bytes, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Attention with Qwen3.5's fused query heads and sigmoid output gate (the
+ * epilogue of the attention block).  The CPU reference reads query head h of
+ * token i in place at q + (i*n_heads + h)*q_stride (q_stride = 2*head_dim when
+ * the projection interleaves [query | gate] per head) and multiplies the
+ * head's output by sigmoid(gate), gate being the second half of the same pair
+ * (qwen35/cpu.rs:333-337, 359-363; sigmoid ops.rs:181-183).  The GPU reference
+ * deinterleaves with split_half and gates with mul_sigmoid (ops.wgsl:150-184,
+ * recorded at qwen35.rs:1012-1028 and 1098-1107): three more dispatches and
+ * two more passes over the activations.  Here q is read at its stride and the
+ * gate is applied where the output is written; no extra pass.
+ *   x == NULL is lmx_attn_fwd.  Else:
+ *   q_stride     elements between consecutive query heads (0: head_dim);
+ *                a multiple of 8, >= head_dim
+ *   gate         NULL: no gate; else out[i,h,d] *= 1/(1+exp(-g)) with
+ *                g = gate[(i*n_heads + h)*gate_stride + d], 16-byte aligned
+ *   gate_stride  floats between consecutive gate heads (0: head_dim);
+ *                a multiple of 4, >= head_dim
+ * gate may point into q's buffer (q + head_dim for the fused layout); out may
+ * not overlap q or gate.  Same workspace as lmx_attn_fwd. */
+typedef struct {
+    uint32_t q_stride;
+    uint32_t gate_stride;
+    const float *gate;
+} lmx_attn_ext;
+
+lmx_status lmx_attn_fwd_ext(const lmx_attn_params *p, const lmx_attn_ext *x, const void *q,
+                            lmx_dtype q_dt, const void *k_cache, const void *v_cache,
+                            lmx_dtype kv_dt, const void *k_cur, const void *v_cur, float *out,
+                            void *ws, size_t ws_bytes, lmx_stream stream);
 
 /* ------------------------------------------------------------------------
  * Ragged multi-sequence decode: one query token per sequence, each sequence

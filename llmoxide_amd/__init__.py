@@ -136,6 +136,15 @@ class DeltaFrontDesc(ctypes.Structure):
     ]
 
 
+class AttnExt(ctypes.Structure):
+    """lmx_attn_ext: query head stride and optional sigmoid output gate."""
+    _fields_ = [
+        ("q_stride", ctypes.c_uint32),
+        ("gate_stride", ctypes.c_uint32),
+        ("gate", ctypes.c_void_p),
+    ]
+
+
 class DeltaBackDesc(ctypes.Structure):
     """lmx_delta_back_desc: the gated RMS norm after the recurrence."""
     _fields_ = [
@@ -151,6 +160,7 @@ _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.
 _PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINTER(Dop)
 _PP = ctypes.POINTER(PrologueDesc)
 _PF, _PB = ctypes.POINTER(DeltaFrontDesc), ctypes.POINTER(DeltaBackDesc)
+_PX = ctypes.POINTER(AttnExt)
 SIGNATURES = {
     "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "lmx_version": (ctypes.c_int, []),
@@ -161,6 +171,8 @@ SIGNATURES = {
     "lmx_attn_workspace_bytes": (_SZ, [_PA]),
     "lmx_attn_fwd": (ctypes.c_int, [_PA, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP, _VP, _VP,
                                     _VP, _SZ, _VP]),
+    "lmx_attn_fwd_ext": (ctypes.c_int, [_PA, _PX, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP,
+                                        _VP, _VP, _VP, _SZ, _VP]),
     "lmx_attn_decode_batched_workspace_bytes": (_SZ, [_PA, _I32, _I32]),
     "lmx_attn_decode_batched": (ctypes.c_int, [_PA, _I32, _I32, _VP, _VP, _VP, _VP, ctypes.c_int,
                                                ctypes.c_int, _VP, _VP, _SZ, _VP]),
@@ -302,11 +314,17 @@ def attn_prologue(q, k_new, v_new, k_cache, v_cache, *, n_heads: int, n_kv_heads
 def attention(q, k_cache, v_cache, *, n_heads: int, n_kv_heads: int, head_dim: int,
               base_pos: int, window: int = 0, bidi: bool = False, scale: Optional[float] = None,
               k_cur=None, v_cur=None, out=None, workspace: Optional[Workspace] = None,
-              kv_dim: Optional[int] = None, stream=None):
+              kv_dim: Optional[int] = None, q_stride: Optional[int] = None, gate=None,
+              gate_stride: Optional[int] = None, stream=None):
     """GQA attention of q [t, H*hd] (f32/f16) over f16 caches [n_slots, kv_dim].
 
     Returns out [t, H*hd] f32.  The semantics are the reference's CPU attention
     (cpu.rs:342-387; qwen35/cpu.rs:324-365); see include/lmx/attn.h.
+
+    ``q_stride`` reads query head h of token i at element (i*H + h)*q_stride of
+    ``q`` (qwen35's fused [query | gate] heads: 2*hd), and ``gate`` (f32, read
+    at (i*H + h)*gate_stride + d) scales the output by sigmoid(gate)
+    (qwen35/cpu.rs:359-363); both go through lmx_attn_fwd_ext.
     """
     torch = _torch()
     _need_cuda(q, k_cache, v_cache, k_cur, v_cur, out)
@@ -322,9 +340,18 @@ def attention(q, k_cache, v_cache, *, n_heads: int, n_kv_heads: int, head_dim: i
         workspace = workspace or Workspace(device=q.device)
         workspace.ensure(need, stream)
         ws_ptr, ws_bytes = workspace.base, workspace.nbytes
-    rc = lib().lmx_attn_fwd(ctypes.byref(p), _ptr(q), _dt(q), _ptr(k_cache), _ptr(v_cache), F16,
-                            _ptr(k_cur), _ptr(v_cur), _ptr(out), ws_ptr, ws_bytes, _stream(stream))
-    _check("lmx_attn_fwd", rc)
+    if q_stride is None and gate is None and gate_stride is None:
+        rc = lib().lmx_attn_fwd(ctypes.byref(p), _ptr(q), _dt(q), _ptr(k_cache), _ptr(v_cache), F16,
+                                _ptr(k_cur), _ptr(v_cur), _ptr(out), ws_ptr, ws_bytes,
+                                _stream(stream))
+        _check("lmx_attn_fwd", rc)
+        return out
+    _need_cuda(gate)
+    x = AttnExt(q_stride or 0, gate_stride or 0, _ptr(gate))
+    rc = lib().lmx_attn_fwd_ext(ctypes.byref(p), ctypes.byref(x), _ptr(q), _dt(q), _ptr(k_cache),
+                                _ptr(v_cache), F16, _ptr(k_cur), _ptr(v_cur), _ptr(out), ws_ptr,
+                                ws_bytes, _stream(stream))
+    _check("lmx_attn_fwd_ext", rc)
     return out
 
 

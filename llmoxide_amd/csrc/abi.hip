@@ -13,17 +13,17 @@ namespace lmx {
 // attn_decode.hip
 size_t decode_workspace_bytes(const lmx_attn_params* p);
 size_t decode_batched_workspace_bytes(const lmx_attn_params* p, int n_seq, int max_ctx);
-lmx_status decode_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
-                      const void* v_cache, const void* k_cur, const void* v_cur, float* out,
-                      void* ws, size_t ws_bytes, hipStream_t st);
+lmx_status decode_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
+                      const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
+                      float* out, void* ws, size_t ws_bytes, hipStream_t st);
 lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, const int32_t* ctx_lens,
                           const void* const* k_ptrs, const void* const* v_ptrs, const void* q,
                           lmx_dtype q_dt, float* out, void* ws, size_t ws_bytes, hipStream_t st);
 // attn_prefill.hip
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt);
-lmx_status prefill_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
-                       const void* v_cache, const void* k_cur, const void* v_cur, float* out,
-                       hipStream_t st);
+lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
+                       const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
+                       float* out, hipStream_t st);
 // deltanet.hip
 lmx_status deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
                           const float* alpha, const float* beta, const float* conv, float* state,
@@ -51,6 +51,12 @@ lmx_status deltanet_back(const lmx_delta_back_desc* d, float* o, const float* z,
 constexpr uint32_t kSplitKMaxTokens = 8;
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// [a, a + na) and [b, b + nb) share a byte.
+static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+    const char *ca = static_cast<const char*>(a), *cb = static_cast<const char*>(b);
+    return ca < cb + nb && cb < ca + na;
+}
 
 static lmx_status check_attn_params(const lmx_attn_params* p) {
     if (!p) return LMX_E_NULL;
@@ -130,7 +136,7 @@ const char* lmx_status_str(lmx_status s) {
     return "unknown status";
 }
 
-int lmx_version(void) { return 102; }
+int lmx_version(void) { return 103; }
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
@@ -224,6 +230,14 @@ lmx_status lmx_attn_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt,
                         const void* k_cache, const void* v_cache, lmx_dtype kv_dt,
                         const void* k_cur, const void* v_cur, float* out, void* ws,
                         size_t ws_bytes, lmx_stream stream) {
+    return lmx_attn_fwd_ext(p, nullptr, q, q_dt, k_cache, v_cache, kv_dt, k_cur, v_cur, out, ws,
+                            ws_bytes, stream);
+}
+
+lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, const void* q,
+                            lmx_dtype q_dt, const void* k_cache, const void* v_cache,
+                            lmx_dtype kv_dt, const void* k_cur, const void* v_cur, float* out,
+                            void* ws, size_t ws_bytes, lmx_stream stream) {
     lmx_status s = check_attn_params(p);
     if (s != LMX_OK) return s;
     if (q_dt != LMX_F32 && q_dt != LMX_F16) return LMX_E_UNSUPPORTED;
@@ -235,10 +249,30 @@ lmx_status lmx_attn_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt,
     if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 16))
         return LMX_E_ALIGN;
     if (k_cur && (!aligned(k_cur, 16) || !aligned(v_cur, 16))) return LMX_E_ALIGN;
+    const uint32_t hd = p->head_dim;
+    AttnIo io{(int)hd, (int)hd, nullptr};
+    if (x) {
+        const uint32_t qs = x->q_stride ? x->q_stride : hd;
+        const uint32_t gs = x->gate_stride ? x->gate_stride : hd;
+        if (qs < hd || qs % 8 || gs < hd || gs % 4) return LMX_E_SHAPE;
+        if ((uint64_t)p->n_tokens * p->n_heads * qs > INT32_MAX ||
+            (uint64_t)p->n_tokens * p->n_heads * gs > INT32_MAX)
+            return LMX_E_SHAPE;
+        if (x->gate && !aligned(x->gate, 16)) return LMX_E_ALIGN;
+        // out must not overlap what the kernels read after writing it
+        const size_t q_bytes = ((size_t)p->n_tokens * p->n_heads - 1) * qs * (q_dt == LMX_F32 ? 4 : 2) +
+                               (size_t)hd * (q_dt == LMX_F32 ? 4 : 2);
+        const size_t o_bytes = (size_t)p->n_tokens * p->n_heads * hd * 4;
+        if (overlaps(out, o_bytes, q, q_bytes)) return LMX_E_SHAPE;
+        if (x->gate && overlaps(out, o_bytes, x->gate,
+                                (((size_t)p->n_tokens * p->n_heads - 1) * gs + hd) * 4))
+            return LMX_E_SHAPE;
+        io = AttnIo{(int)qs, (int)gs, x->gate};
+    }
     if (use_split_k(p, q_dt))
-        return decode_fwd(p, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
+        return decode_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
                           (hipStream_t)stream);
-    return prefill_fwd(p, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, (hipStream_t)stream);
+    return prefill_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, (hipStream_t)stream);
 }
 
 size_t lmx_attn_decode_batched_workspace_bytes(const lmx_attn_params* p, int32_t n_seq,
@@ -328,9 +362,8 @@ lmx_status lmx_deltanet_front(const lmx_delta_front_desc* d, const float* x, con
                           (const void*)conv_out})
         if (!aligned(p, 4)) return LMX_E_ALIGN;
     // the batch rows are read by later tokens' taps: the output must not overlay them
-    const char *xb = (const char*)x, *ob = (const char*)conv_out;
     const size_t bytes = (size_t)d->n_tok * d->conv_dim * sizeof(float);
-    if (ob < xb + bytes && xb < ob + bytes) return LMX_E_SHAPE;
+    if (overlaps(conv_out, bytes, x, bytes)) return LMX_E_SHAPE;
     return deltanet_front(d, x, taps, conv_state, conv_out, (hipStream_t)stream);
 }
 

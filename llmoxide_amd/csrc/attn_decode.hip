@@ -173,11 +173,14 @@ static lmx_status run(DecodeArgs a, const DecodePlan& pl, int n_q, int hd, lmx_d
     return LMX_OK;
 }
 
-lmx_status decode_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
-                      const void* v_cache, const void* k_cur, const void* v_cur, float* out,
-                      void* ws, size_t ws_bytes, hipStream_t st) {
+lmx_status decode_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
+                      const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
+                      float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     DecodeArgs a{};
     a.q = q;
+    a.q_stride = io.q_stride;
+    a.gate = io.gate;
+    a.gate_stride = io.gate_stride;
     a.k = static_cast<const f16*>(k_cache);
     a.v = static_cast<const f16*>(v_cache);
     a.k_cur = static_cast<const f16*>(k_cur);
@@ -207,6 +210,7 @@ lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, cons
                           lmx_dtype q_dt, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     DecodeArgs a{};
     a.q = q;
+    a.q_stride = (int)p->head_dim;
     a.k_ptrs = reinterpret_cast<const f16* const*>(k_ptrs);
     a.v_ptrs = reinterpret_cast<const f16* const*>(v_ptrs);
     a.ctx_lens = ctx_lens;

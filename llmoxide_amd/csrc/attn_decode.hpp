@@ -65,6 +65,9 @@ struct DecodeArgs {
     const f16* v_cur;
     const int32_t* ctx_lens;
     float* out;
+    const float* gate;      // NULL, or the output gate: out *= sigmoid(gate[row * gate_stride + d])
+    int q_stride;           // elements between consecutive query heads
+    int gate_stride;
     float* part_o;          // [n_q][H][P][HD]  per-split partials
     float* part_ml;         // [n_q][H][P][2]   (max in log2 units, sum)
     int H, Hkv, G, kv_dim;
@@ -234,8 +237,9 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
     }
     if (merge && part == 0) {
         const float inv = 1.f / l_run;
-        *reinterpret_cast<f32x4*>(a.out + row * HD + d0) =
-            f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        f32x4 y = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        if (a.gate) y = gate_sigmoid4(y, a.gate + row * a.gate_stride + d0);
+        *reinterpret_cast<f32x4*>(a.out + row * HD + d0) = y;
     }
 }
 
@@ -363,7 +367,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
             const int head = (kvg * HW + e_hs) * a.G + hb * GB + g;
             const size_t row = (size_t)qi * a.H + head;
             if (p_u == 1) {
-                a.out[row * HD + d] = O / Lw;
+                const float y = O / Lw;
+                a.out[row * HD + d] = a.gate ? gate_sigmoid(y, a.gate[row * a.gate_stride + d]) : y;
             } else {
                 const size_t pidx = row * a.P + split;
                 a.part_o[pidx * HD + d] = O;
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         QRaw qraw[KS][QN];
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            const size_t qo = ((size_t)qi * a.H + qhead) * HD + 32 * s + 8 * g4;
+            const size_t qo = ((size_t)qi * a.H + qhead) * a.q_stride + 32 * s + 8 * g4;
             if constexpr (SPLIT_Q) {
                 const float* qp = reinterpret_cast<const float*>(a.q) + qo;
                 qraw[s][0] = *reinterpret_cast<const f32x4*>(qp);
@@ -585,11 +590,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
                         float* dst = p_u == 1 ? a.out + row * HD + d0
                                               : a.part_o + (row * a.P + split) * HD + d0;
 #pragma unroll
-                        for (int j = 0; j < VW; j += 4)
-                            *reinterpret_cast<f32x4*>(dst + j) =
-                                p_u == 1 ? f32x4{acc[j] * inv, acc[j + 1] * inv, acc[j + 2] * inv,
-                                                 acc[j + 3] * inv}
-                                         : f32x4{acc[j], acc[j + 1], acc[j + 2], acc[j + 3]};
+                        for (int j = 0; j < VW; j += 4) {
+                            f32x4 y = p_u == 1 ? f32x4{acc[j] * inv, acc[j + 1] * inv, acc[j + 2] * inv,
+                                                       acc[j + 3] * inv}
+                                               : f32x4{acc[j], acc[j + 1], acc[j + 2], acc[j + 3]};
+                            if (p_u == 1 && a.gate) y = gate_sigmoid4(y, a.gate + row * a.gate_stride + d0 + j);
+                            *reinterpret_cast<f32x4*>(dst + j) = y;
+                        }
                     }
                 }
             }

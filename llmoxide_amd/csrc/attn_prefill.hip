@@ -29,6 +29,8 @@ struct PrefillArgs {
     const f16* k_cur;
     const f16* v_cur;
     float* out;
+    const float* gate;  // NULL, or the output gate: out *= sigmoid(gate[row * gate_stride + d])
+    int q_stride, gate_stride;
     int H, Hkv, G, kv_dim;
     int base_pos, window, n_tokens, bidi;
     int n_qtiles;
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     // for Q alone), so the S^T accumulators are already exp2 arguments.
     f16x8 qf[KSTEPS];
     {
-        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * HD + 8 * hh;
+        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             float x[8];
@@ -323,13 +325,17 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     if (!qvalid) return;
     const float inv = 1.f / l_tot;
     float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
+    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride : nullptr;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4)
-            *reinterpret_cast<f32x4*>(orow + nb * 32 + 8 * g4 + 4 * hh) =
-                f32x4{o[nb][4 * g4] * inv, o[nb][4 * g4 + 1] * inv, o[nb][4 * g4 + 2] * inv,
-                      o[nb][4 * g4 + 3] * inv};
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = nb * 32 + 8 * g4 + 4 * hh;
+            f32x4 y = f32x4{o[nb][4 * g4] * inv, o[nb][4 * g4 + 1] * inv, o[nb][4 * g4 + 2] * inv,
+                            o[nb][4 * g4 + 3] * inv};
+            if (grow) y = gate_sigmoid4(y, grow + d);
+            *reinterpret_cast<f32x4*>(orow + d) = y;
+        }
 }
 
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
@@ -337,11 +343,14 @@ bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
     return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
 }
 
-lmx_status prefill_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt, const void* k_cache,
-                       const void* v_cache, const void* k_cur, const void* v_cur, float* out,
-                       hipStream_t st) {
+lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
+                       const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
+                       float* out, hipStream_t st) {
     PrefillArgs a{};
     a.q = q;
+    a.q_stride = io.q_stride;
+    a.gate = io.gate;
+    a.gate_stride = io.gate_stride;
     a.k = static_cast<const f16*>(k_cache);
     a.v = static_cast<const f16*>(v_cache);
     a.k_cur = static_cast<const f16*>(k_cur);

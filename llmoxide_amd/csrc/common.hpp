@@ -54,6 +54,15 @@ __device__ __forceinline__ float wave_sum64(float x) {
 
 __device__ __forceinline__ float shfl_xor(float x, int m) { return __shfl_xor(x, m, 64); }
 
+// Qwen3.5's attention output gate: o * sigmoid(g), written as the GPU
+// reference's mul_sigmoid writes it, o / (1 + exp(-g)) (ops.wgsl:150-163).
+__device__ __forceinline__ float gate_sigmoid(float o, float g) { return o / (1.f + expf(-g)); }
+__device__ __forceinline__ f32x4 gate_sigmoid4(f32x4 o, const float* g) {
+    const f32x4 gv = *reinterpret_cast<const f32x4*>(g);
+    return f32x4{gate_sigmoid(o[0], gv[0]), gate_sigmoid(o[1], gv[1]), gate_sigmoid(o[2], gv[2]),
+                 gate_sigmoid(o[3], gv[3])};
+}
+
 // Load N consecutive f16 values (N a multiple of 4) as floats.
 template <int N>
 __device__ __forceinline__ void load_f16_as_f32(const f16* __restrict__ p, float (&out)[N]) {
@@ -112,6 +121,14 @@ template <int N>
 __device__ __forceinline__ float raw_at(const RawF16<N>& r, int i) {
     return (float)r.v[i / 4][i % 4];
 }
+
+// Where an attention call reads q and gates its output (lmx_attn_ext,
+// resolved: strides in elements, gate NULL when there is none).
+struct AttnIo {
+    int q_stride;
+    int gate_stride;
+    const float* gate;
+};
 
 }  // namespace lmx
 

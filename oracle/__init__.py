@@ -112,6 +112,7 @@ def lib() -> ctypes.CDLL:
         L.orc_attn_prologue.argtypes = [P(OrcPrologue), f32p, f32p, f32p, f32p, f32p, f32p, u16p, u16p]
         L.orc_delta_front.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_float] + [f32p] * 4
         L.orc_delta_back.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_float] + [f32p] * 3
+        L.orc_attn_gate.argtypes = [ctypes.c_int64] * 3 + [f32p] * 2
         _lib = L
     return _lib
 
@@ -286,6 +287,18 @@ def delta_front(x, taps, state, *, key_dim, s_dim, eps=1e-6):
     lib().orc_delta_front(t, conv_dim, key_dim, s_dim, kernel, eps, _f32p(x), _f32p(taps), _f32p(st),
                           _f32p(out))
     return out, st
+
+
+def attn_gate(out, gate, *, dim, gate_stride=None):
+    """Qwen3.5's attention output gate (qwen35/cpu.rs:359-363): each row of
+    ``out`` [rows, dim] times sigmoid(gate row), the gate row r starting at
+    element r*gate_stride of ``gate``.  Returns a new array."""
+    out = np.ascontiguousarray(out, np.float32).reshape(-1, dim).copy()
+    gate = np.ascontiguousarray(gate, np.float32).reshape(-1)
+    gs = gate_stride or dim
+    assert gate.size >= (out.shape[0] - 1) * gs + dim
+    lib().orc_attn_gate(out.shape[0], dim, gs, _f32p(out), _f32p(gate))
+    return out
 
 
 def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):

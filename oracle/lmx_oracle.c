@@ -44,6 +44,11 @@
  *                        q/k heads).
  *   orc_delta_back       crates/model/src/qwen35/cpu.rs:250-259 (gated RMS
  *                        norm), pinned by a float64 restatement.
+ *   orc_attn_gate        crates/model/src/qwen35/cpu.rs:359-363 with
+ *                        ops::sigmoid (ops.rs:181-183): the attention output
+ *                        times sigmoid(gate); pinned by its special values
+ *                        (gate 0 halves, large gates pass or zero) and a
+ *                        float64 restatement.
  *   orc_delta_recur      crates/model/src/qwen35/cpu.rs:218-245 (and the GPU
  *                        form deltanet.wgsl:193-239), pinned by a float64
  *                        matrix restatement and by invariants (exact write at
@@ -476,6 +481,19 @@ void orc_delta_front(int64_t n_tok, int64_t conv_dim, int64_t key_dim, int64_t s
 
 /* qwen35/cpu.rs:250-259: per token and v-head, rms_norm_mul(o, w) then
  * o *= silu(z), in place. */
+/* out[r][d] *= sigmoid(gate[r*gate_stride + d]) for r < n_rows, d < dim, in
+ * the reference's order: sigmoid(x) = 1 / (1 + exp(-x)) in f32, then the
+ * product (qwen35/cpu.rs:359-363, ops.rs:181-183). */
+void orc_attn_gate(int64_t n_rows, int64_t dim, int64_t gate_stride, float *out,
+                   const float *gate) {
+    for (int64_t r = 0; r < n_rows; ++r)
+        for (int64_t d = 0; d < dim; ++d) {
+            const float g = gate[r * gate_stride + d];
+            const float s = 1.0f / (1.0f + expf(-g));
+            out[r * dim + d] *= s;
+        }
+}
+
 void orc_delta_back(int64_t n_tok, int64_t n_vh, int64_t s_dim, float eps, float *o,
                     const float *z, const float *w) {
     for (int64_t r = 0; r < n_tok * n_vh; ++r) {

@@ -202,6 +202,15 @@ def delta_front(x, taps, state, *, key_dim, s_dim, eps=1e-6):
     return out, full[t:]
 
 
+def attn_gate(out, gate, *, dim, gate_stride=None):
+    """out * sigmoid(gate) in float64, gate row r at element r*gate_stride."""
+    out = np.asarray(out, np.float64).reshape(-1, dim)
+    gs = gate_stride or dim
+    g = np.stack([np.asarray(gate, np.float64).reshape(-1)[r * gs:r * gs + dim]
+                  for r in range(out.shape[0])])
+    return out / (1.0 + np.exp(-g))
+
+
 def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):
     o = np.asarray(o, np.float64).reshape(-1, n_vh, s_dim)
     z = np.asarray(z, np.float64).reshape(o.shape)

@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 14
+    assert len(names) == 15
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = lmx.lib()
-    assert L.lmx_version() == 102
+    assert L.lmx_version() == 103
     for s in lmx.Status:
         assert L.lmx_status_str(int(s))
     assert L.lmx_status_str(999) == b"unknown status"
@@ -86,6 +86,34 @@ def test_attn_fwd_rejects_bad_pointers_and_dtypes():
     assert _fwd(p, kvdt=lmx.F32) == lmx.Status.E_UNSUPPORTED
     assert _fwd(p, qdt=7) == lmx.Status.E_UNSUPPORTED
     assert lmx.lib().lmx_attn_fwd(None, FAKE, 0, FAKE, FAKE, 1, None, None, FAKE, None, 0, None) == lmx.Status.E_NULL
+
+
+def _fwd_ext(p, ext, q=FAKE, out=FAKE + (1 << 24)):
+    x = lmx.AttnExt(**ext)
+    return lmx.lib().lmx_attn_fwd_ext(ctypes.byref(p), ctypes.byref(x), q, lmx.F32, FAKE, FAKE,
+                                      lmx.F16, None, None, out, None, 0, None)
+
+
+GATE = FAKE + (1 << 26)
+
+
+@pytest.mark.parametrize("ext,code", [
+    (dict(q_stride=64), lmx.Status.E_SHAPE),                     # below head_dim
+    (dict(q_stride=132), lmx.Status.E_SHAPE),                    # not a multiple of 8
+    (dict(gate_stride=130, gate=GATE), lmx.Status.E_SHAPE),      # not a multiple of 4
+    (dict(gate_stride=64, gate=GATE), lmx.Status.E_SHAPE),       # below head_dim
+    (dict(q_stride=256, gate=GATE + 4), lmx.Status.E_ALIGN),     # gate not 16-byte aligned
+])
+def test_attn_fwd_ext_rejects_bad_layouts(ext, code):
+    assert _fwd_ext(_params(), ext) == code
+
+
+def test_attn_fwd_ext_rejects_out_overlapping_q_or_gate():
+    p = _params(n_tokens=2, n_slots=64, base_pos=10)
+    # the fused [query | gate] rows of 2 tokens x 32 heads x 256 floats
+    assert _fwd_ext(p, dict(q_stride=256), out=FAKE + 4096) == lmx.Status.E_SHAPE
+    assert _fwd_ext(p, dict(q_stride=256, gate=GATE, gate_stride=256),
+                    out=GATE + 1024) == lmx.Status.E_SHAPE
 
 
 def test_decode_needs_workspace_when_split():
