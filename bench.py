@@ -188,6 +188,32 @@ def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
     return {"t": t, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_kvm(lmx, torch, which, steps=20, warmup=3):
+    """KV manager.  "wipe": zeroing one Qwen3-8B sequence slab (36 layers of
+    f16 K and V at 32k positions, 4.83 GB) with lmx_kvm_wipe, an HBM write.
+    "batch": host time of lmx_kvm_batch for a ragged batch of 32 sequences."""
+    layers = [(0, HKV * HD, -1)] * N_LAYERS
+    if which == "wipe":
+        m = lmx.KvManager(layers, n_ctx=CTX, max_seqs=1)
+        s = m.open()
+        ms = time_calls([lambda: m.wipe(s)], steps, warmup, torch)
+        nbytes = m.arena_bytes
+        del m
+        return {"bytes": nbytes, "ms": ms, "GB/s": nbytes / (ms * 1e-3) / 1e9,
+                "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    m = lmx.KvManager(layers, n_ctx=CTX, max_seqs=32, arena=(1 << 20, 1 << 48))
+    seqs = [m.open() for _ in range(32)]
+    for i, s in enumerate(seqs):
+        m.commit(s, list(range(100 + 900 * i)))
+    for _ in range(warmup):
+        m.batch(0, seqs)
+    t0 = time.perf_counter()
+    for _ in range(steps * 50):
+        m.batch(0, seqs)
+    us = (time.perf_counter() - t0) / (steps * 50) * 1e6
+    return {"B": 32, "host_us_per_batch_table": us}
+
+
 def bench_delta_io(lmx, torch, T, which, steps=20, warmup=3):
     """Delta-net front (conv + SiLU + window + q/k L2 norm) or back (gated RMS
     norm) at C5.  Bytes: front reads x and writes conv_out (f32 [T, 8192]),
@@ -315,6 +341,8 @@ def main():
             ("delta_decode_1tok", lambda: bench_delta(lmx, torch, 1, False, steps=50, warmup=5)),
             ("delta_front_T4096", lambda: bench_delta_io(lmx, torch, 4096, "front")),
             ("delta_back_T4096", lambda: bench_delta_io(lmx, torch, 4096, "back")),
+            ("kvm_wipe_qwen3_8b_32k", lambda: bench_kvm(lmx, torch, "wipe")),
+            ("kvm_batch_tables_b32", lambda: bench_kvm(lmx, torch, "batch")),
         ]:
             if args.extras and name not in args.extras.split(","):
                 continue

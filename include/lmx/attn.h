@@ -46,7 +46,9 @@ typedef enum {
     LMX_E_RING_HAZARD = 6,    /* windowed batch would read overwritten slots   */
     LMX_E_ALIGN = 7,          /* pointer not aligned as the layout requires     */
     LMX_E_LAUNCH = 8,         /* the HIP runtime rejected a launch              */
-    LMX_E_DEVICE = 9          /* no usable gfx950 device                        */
+    LMX_E_DEVICE = 9,         /* no usable gfx950 device                        */
+    LMX_E_FULL = 10,          /* no free sequence slot in a KV manager          */
+    LMX_E_HOST = 11           /* host memory for bookkeeping ran out            */
 } lmx_status;
 
 typedef enum { LMX_F32 = 0, LMX_F16 = 1 } lmx_dtype;
@@ -298,6 +300,96 @@ typedef struct {
 
 lmx_status lmx_deltanet_back(const lmx_delta_back_desc *d, float *o, const float *z,
                              const float *w, lmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Multi-sequence KV manager.  The reference serves one sequence at a time
+ * (docs/limitations.md:21): one KvCache per session (cache.rs:65-154), sized
+ * per layer as kv_slots (config.rs:279-284: min(window, n_ctx) ring slots for
+ * a windowed layer, n_ctx for a global one), with layers that share an
+ * earlier layer's cache allocating nothing (cache.rs:86-104), and the
+ * session's prefix reuse (session.rs:497-513, 546-570).  This keeps that
+ * bookkeeping for up to max_seqs sequences whose f16 caches live in one
+ * caller-allocated device arena, and hands out what the attention entry
+ * points take: a sequence's per-layer cache pointers for appends, prologues
+ * and prefill, and the pointer / length tables of lmx_attn_decode_batched for
+ * a ragged batch.
+ *
+ * HBM layout: sequence s owns bytes [s*slab, (s+1)*slab) of the arena; inside
+ * it every cache-owning layer has a K block then a V block of
+ * [slots, kv_dim] f16 rows (the reference's row-major-by-slot layout,
+ * cache.rs:10-18), each block 256-byte aligned.  Host bookkeeping only: no
+ * call but lmx_kvm_wipe/lmx_kvm_begin enqueues device work, none allocates
+ * device memory, none synchronizes.  A manager is not thread-safe; calls on
+ * one manager must be serialized by the caller. */
+typedef struct lmx_kvm lmx_kvm;
+
+typedef struct {
+    uint32_t window;     /* 0: global (linear, n_ctx slots); else ring of min(window, n_ctx) */
+    uint32_t kv_dim;     /* elements per cache row (a multiple of 8)                          */
+    int32_t kv_source;   /* -1: owns its cache; else an earlier layer whose cache it reads    */
+} lmx_kvm_layer;
+
+typedef struct {
+    uint32_t n_layers;
+    uint32_t n_ctx;              /* positions per sequence                 */
+    uint32_t max_seqs;           /* sequence slots in the arena            */
+    const lmx_kvm_layer *layers; /* [n_layers]                             */
+} lmx_kvm_desc;
+
+/* Device bytes the arena needs (0 for an invalid description). */
+size_t lmx_kvm_arena_bytes(const lmx_kvm_desc *d);
+
+lmx_status lmx_kvm_create(const lmx_kvm_desc *d, void *arena, size_t arena_bytes, lmx_kvm **out);
+void lmx_kvm_destroy(lmx_kvm *m);
+
+/* Claim an empty sequence slot (LMX_E_FULL when none is free) / release one. */
+lmx_status lmx_kvm_open(lmx_kvm *m, int32_t *seq);
+lmx_status lmx_kvm_close(lmx_kvm *m, int32_t seq);
+
+/* Positions written so far: the next token lands at this position. */
+lmx_status lmx_kvm_len(const lmx_kvm *m, int32_t seq, uint32_t *len);
+
+/* session.rs:497-513: how much of the prompt tokens[0, n) the resident cache
+ * serves.  Only a strict prefix of what is resident counts (ring layers have
+ * already overwritten anything before a rewind point), and nothing once an
+ * embedding span made the resident ids incomplete. */
+lmx_status lmx_kvm_reusable_prefix(const lmx_kvm *m, int32_t seq, const int32_t *tokens,
+                                   uint32_t n, uint32_t *reuse);
+
+/* A new turn with prompt tokens[0, n) (session.rs:546-553): *reuse is the
+ * reusable prefix; when it is 0 the sequence's caches are overwritten with
+ * zeros on `stream` and its bookkeeping reset, as the reference wipes before
+ * an unrelated conversation.  The caller then runs positions [*reuse, n) and
+ * commits them.  LMX_E_CONTEXT when n > n_ctx. */
+lmx_status lmx_kvm_begin(lmx_kvm *m, int32_t seq, const int32_t *tokens, uint32_t n,
+                         uint32_t *reuse, lmx_stream stream);
+
+/* Record that the caller appended n rows at positions [len, len + n):
+ * len += n and the ids join the resident list (session.rs:568, 607-609).
+ * tokens == NULL marks rows from an embedding span: the sequence stops being
+ * comparable for prefix reuse (session.rs:569-571).  LMX_E_CONTEXT when
+ * len + n > n_ctx. */
+lmx_status lmx_kvm_commit(lmx_kvm *m, int32_t seq, const int32_t *tokens, uint32_t n);
+
+/* cache.rs:146-149: drop everything from pos onward (len = min(len, pos)). */
+lmx_status lmx_kvm_truncate(lmx_kvm *m, int32_t seq, uint32_t pos);
+
+/* cache.rs:138-143: zero the sequence's caches on `stream`, len = 0. */
+lmx_status lmx_kvm_wipe(lmx_kvm *m, int32_t seq, lmx_stream stream);
+
+/* The caches layer `layer` of sequence `seq` reads and writes (a sharing
+ * layer's are its source's): f16 [n_slots, kv_dim]; *window is what
+ * lmx_kv_desc / lmx_attn_params take (0 linear, else the ring size). */
+lmx_status lmx_kvm_layer_cache(const lmx_kvm *m, int32_t seq, uint32_t layer, void **k,
+                               void **v, uint32_t *n_slots, uint32_t *window);
+
+/* Host tables of lmx_attn_decode_batched for layer `layer` over seqs[0, n):
+ * k_ptrs/v_ptrs[b] = the sequence's caches, ctx_lens[b] = its len + extra
+ * (extra: rows appended for this step but not yet committed, 1 for a decode
+ * step), *max_ctx = the largest.  The caller copies the tables to the device. */
+lmx_status lmx_kvm_batch(const lmx_kvm *m, uint32_t layer, const int32_t *seqs, uint32_t n,
+                         uint32_t extra, const void **k_ptrs, const void **v_ptrs,
+                         int32_t *ctx_lens, int32_t *max_ctx);
 
 #ifdef __cplusplus
 }

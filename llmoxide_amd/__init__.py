@@ -34,7 +34,7 @@ import ctypes
 import enum
 import math
 import os
-from typing import Optional, Sequence
+from typing import Optional, Sequence, Tuple
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllmoxide_amd.so")
@@ -51,6 +51,8 @@ class Status(enum.IntEnum):
     E_ALIGN = 7
     E_LAUNCH = 8
     E_DEVICE = 9
+    E_FULL = 10
+    E_HOST = 11
 
 
 F32, F16 = 0, 1
@@ -145,6 +147,25 @@ class AttnExt(ctypes.Structure):
     ]
 
 
+class KvmLayer(ctypes.Structure):
+    """lmx_kvm_layer: one layer of a KV manager (window, row size, sharing)."""
+    _fields_ = [
+        ("window", ctypes.c_uint32),
+        ("kv_dim", ctypes.c_uint32),
+        ("kv_source", ctypes.c_int32),
+    ]
+
+
+class KvmDesc(ctypes.Structure):
+    """lmx_kvm_desc: layers, positions per sequence and sequence slots."""
+    _fields_ = [
+        ("n_layers", ctypes.c_uint32),
+        ("n_ctx", ctypes.c_uint32),
+        ("max_seqs", ctypes.c_uint32),
+        ("layers", ctypes.POINTER(KvmLayer)),
+    ]
+
+
 class DeltaBackDesc(ctypes.Structure):
     """lmx_delta_back_desc: the gated RMS norm after the recurrence."""
     _fields_ = [
@@ -161,6 +182,8 @@ _PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINT
 _PP = ctypes.POINTER(PrologueDesc)
 _PF, _PB = ctypes.POINTER(DeltaFrontDesc), ctypes.POINTER(DeltaBackDesc)
 _PX = ctypes.POINTER(AttnExt)
+_PKD, _PI32, _PU32 = ctypes.POINTER(KvmDesc), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_uint32)
+_PVP = ctypes.POINTER(ctypes.c_void_p)
 SIGNATURES = {
     "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "lmx_version": (ctypes.c_int, []),
@@ -179,6 +202,19 @@ SIGNATURES = {
     "lmx_deltanet_recur": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "lmx_deltanet_front": (ctypes.c_int, [_PF, _VP, _VP, _VP, _VP, _VP]),
     "lmx_deltanet_back": (ctypes.c_int, [_PB, _VP, _VP, _VP, _VP]),
+    "lmx_kvm_arena_bytes": (_SZ, [_PKD]),
+    "lmx_kvm_create": (ctypes.c_int, [_PKD, _VP, _SZ, _PVP]),
+    "lmx_kvm_destroy": (None, [_VP]),
+    "lmx_kvm_open": (ctypes.c_int, [_VP, _PI32]),
+    "lmx_kvm_close": (ctypes.c_int, [_VP, _I32]),
+    "lmx_kvm_len": (ctypes.c_int, [_VP, _I32, _PU32]),
+    "lmx_kvm_reusable_prefix": (ctypes.c_int, [_VP, _I32, _PI32, _U32, _PU32]),
+    "lmx_kvm_begin": (ctypes.c_int, [_VP, _I32, _PI32, _U32, _PU32, _VP]),
+    "lmx_kvm_commit": (ctypes.c_int, [_VP, _I32, _PI32, _U32]),
+    "lmx_kvm_truncate": (ctypes.c_int, [_VP, _I32, _U32]),
+    "lmx_kvm_wipe": (ctypes.c_int, [_VP, _I32, _VP]),
+    "lmx_kvm_layer_cache": (ctypes.c_int, [_VP, _I32, _U32, _PVP, _PVP, _PU32, _PU32]),
+    "lmx_kvm_batch": (ctypes.c_int, [_VP, _U32, _PI32, _U32, _U32, _PVP, _PVP, _PI32, _PI32]),
     "lmx_deltanet_chunked_workspace_bytes": (_SZ, [_PD, _I32]),
     "lmx_deltanet_chunked": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I32, _VP, _SZ,
                                             _VP]),
@@ -244,9 +280,9 @@ def _need_cuda(*ts) -> None:
 class Workspace:
     """A zero-initialized device scratch buffer shared by successive calls.
 
-    Calls on one Workspace must be ordered on one stream (the library leaves
-    its counters at zero after each call, so no re-clear is needed between
-    calls).  It grows on demand; growth re-allocates and re-clears.
+    Calls on one Workspace must be ordered on one stream (each call writes
+    every workspace byte it later reads).  It grows on demand; growth
+    re-allocates and re-clears.
     """
 
     def __init__(self, nbytes: int = 0, device=None):
@@ -365,6 +401,18 @@ class BatchedCaches:
         self.k_ptrs = torch.tensor([c.data_ptr() for c in self.k_caches], dtype=torch.int64, device=dev)
         self.v_ptrs = torch.tensor([c.data_ptr() for c in self.v_caches], dtype=torch.int64, device=dev)
 
+    @classmethod
+    def from_addresses(cls, k_ptrs: Sequence[int], v_ptrs: Sequence[int], device=None):
+        """Tables of raw cache addresses (e.g. from :meth:`KvManager.batch`);
+        pass ``n_slots`` to :func:`attention_decode_batched` with them."""
+        torch = _torch()
+        self = cls.__new__(cls)
+        self.k_caches, self.v_caches = [], []
+        dev = device or torch.device("cuda")
+        self.k_ptrs = torch.tensor(list(k_ptrs), dtype=torch.int64, device=dev)
+        self.v_ptrs = torch.tensor(list(v_ptrs), dtype=torch.int64, device=dev)
+        return self
+
 
 def attention_decode_batched(q, caches: BatchedCaches, ctx_lens, *, max_ctx: int, n_heads: int,
                              n_kv_heads: int, head_dim: int, window: int = 0,
@@ -458,3 +506,128 @@ def delta_back(o, z, w, *, n_vh: int, s_dim: int, eps: float = 1e-6, stream=None
     rc = lib().lmx_deltanet_back(ctypes.byref(d), _ptr(o), _ptr(z), _ptr(w), _stream(stream))
     _check("lmx_deltanet_back", rc)
     return o
+
+
+# --------------------------------------------------------------- KV manager --
+def _i32s(xs) -> Tuple[ctypes.Array, int]:
+    xs = list(xs)
+    return (ctypes.c_int32 * max(1, len(xs)))(*xs), len(xs)
+
+
+class KvManager:
+    """Bookkeeping of many sequences' f16 KV caches in one device arena
+    (lmx_kvm_*, include/lmx/attn.h): the reference's per-session KvCache
+    (cache.rs:65-154) and prefix reuse (session.rs:497-513, 546-570), one per
+    sequence slot.
+
+    ``layers`` lists ``(window, kv_dim, kv_source)`` per layer (window 0 for a
+    global layer, kv_source -1 for a layer owning its cache).  The arena is a
+    zeroed device tensor unless ``arena=(address, nbytes)`` names caller memory.
+    """
+
+    def __init__(self, layers, *, n_ctx: int, max_seqs: int, arena=None, device=None):
+        self._layers = (KvmLayer * len(layers))(*[KvmLayer(w, d, s) for (w, d, s) in layers])
+        self.desc = KvmDesc(len(layers), n_ctx, max_seqs, self._layers)
+        self.n_ctx, self.max_seqs = n_ctx, max_seqs
+        self.arena_bytes = lib().lmx_kvm_arena_bytes(ctypes.byref(self.desc))
+        if not self.arena_bytes:
+            raise ValueError("invalid KV manager layout")
+        self.arena_t = None
+        if arena is None:
+            torch = _torch()
+            self.arena_t = torch.zeros(self.arena_bytes + 256, dtype=torch.uint8,
+                                       device=device or torch.device("cuda"))
+            self._off = (-self.arena_t.data_ptr()) % 256
+            base, nbytes = self.arena_t.data_ptr() + self._off, self.arena_bytes
+        else:
+            base, nbytes = arena
+        self.base = base
+        self.h = ctypes.c_void_p()
+        _check("lmx_kvm_create", lib().lmx_kvm_create(ctypes.byref(self.desc), base, nbytes,
+                                                      ctypes.byref(self.h)))
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h and h.value and _lib is not None:
+            _lib.lmx_kvm_destroy(h)
+            self.h = ctypes.c_void_p()
+
+    def open(self) -> int:
+        s = ctypes.c_int32()
+        _check("lmx_kvm_open", lib().lmx_kvm_open(self.h, ctypes.byref(s)))
+        return s.value
+
+    def close(self, seq: int) -> None:
+        _check("lmx_kvm_close", lib().lmx_kvm_close(self.h, seq))
+
+    def len(self, seq: int) -> int:
+        n = ctypes.c_uint32()
+        _check("lmx_kvm_len", lib().lmx_kvm_len(self.h, seq, ctypes.byref(n)))
+        return n.value
+
+    def reusable_prefix(self, seq: int, tokens) -> int:
+        arr, n = _i32s(tokens)
+        r = ctypes.c_uint32()
+        _check("lmx_kvm_reusable_prefix", lib().lmx_kvm_reusable_prefix(self.h, seq, arr, n,
+                                                                        ctypes.byref(r)))
+        return r.value
+
+    def begin(self, seq: int, tokens, stream=None) -> int:
+        arr, n = _i32s(tokens)
+        r = ctypes.c_uint32()
+        _check("lmx_kvm_begin", lib().lmx_kvm_begin(self.h, seq, arr, n, ctypes.byref(r),
+                                                    _stream(stream)))
+        return r.value
+
+    def commit(self, seq: int, tokens=None, n: Optional[int] = None) -> None:
+        if tokens is None:
+            rc = lib().lmx_kvm_commit(self.h, seq, None, int(n))
+        else:
+            arr, cnt = _i32s(tokens)
+            rc = lib().lmx_kvm_commit(self.h, seq, arr, cnt)
+        _check("lmx_kvm_commit", rc)
+
+    def truncate(self, seq: int, pos: int) -> None:
+        _check("lmx_kvm_truncate", lib().lmx_kvm_truncate(self.h, seq, pos))
+
+    def wipe(self, seq: int, stream=None) -> None:
+        _check("lmx_kvm_wipe", lib().lmx_kvm_wipe(self.h, seq, _stream(stream)))
+
+    def layer_cache(self, seq: int, layer: int):
+        """(k address, v address, n_slots, window) of the layer's caches."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        slots, win = ctypes.c_uint32(), ctypes.c_uint32()
+        _check("lmx_kvm_layer_cache", lib().lmx_kvm_layer_cache(
+            self.h, seq, layer, ctypes.byref(k), ctypes.byref(v), ctypes.byref(slots),
+            ctypes.byref(win)))
+        return k.value, v.value, slots.value, win.value
+
+    def layer_tensors(self, seq: int, layer: int):
+        """f16 [n_slots, kv_dim] views of the layer's K and V caches in the arena."""
+        torch = _torch()
+        if self.arena_t is None:
+            raise ValueError("caller-owned arena: use layer_cache() addresses")
+        k, v, slots, _ = self.layer_cache(seq, layer)
+        kv_dim = self._kv_dim(layer)
+        views = []
+        for addr in (k, v):
+            off = addr - self.arena_t.data_ptr()
+            views.append(self.arena_t[off:off + slots * kv_dim * 2].view(torch.float16)
+                         .view(slots, kv_dim))
+        return views[0], views[1]
+
+    def _kv_dim(self, layer: int) -> int:
+        L = self._layers[layer]
+        while L.kv_source >= 0:
+            L = self._layers[L.kv_source]
+        return L.kv_dim
+
+    def batch(self, layer: int, seqs, extra: int = 1):
+        """Host tables for lmx_attn_decode_batched: (k_ptrs, v_ptrs, ctx_lens, max_ctx)."""
+        arr, n = _i32s(seqs)
+        kp, vp = (ctypes.c_void_p * n)(), (ctypes.c_void_p * n)()
+        cl, mx = (ctypes.c_int32 * n)(), ctypes.c_int32()
+        _check("lmx_kvm_batch", lib().lmx_kvm_batch(self.h, layer, arr, n, extra, kp, vp, cl,
+                                                    ctypes.byref(mx)))
+        return list(kp), list(vp), list(cl), mx.value
+

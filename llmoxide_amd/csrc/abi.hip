@@ -89,6 +89,13 @@ __global__ void zero_words(uint32_t* p, size_t n) {
         p[i] = 0u;
 }
 
+// The same for 16-byte aligned buffers of whole 16-byte words (a KV slab).
+__global__ void zero_quads(uint4* p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
 // write_cache (ops.wgsl:323-346): four elements per thread, f32 -> f16 RNE.
 // Row i is skipped when row i + window of the same call maps to the same ring
 // slot, so the latest position wins as in the reference's in-order store.
@@ -132,22 +139,29 @@ const char* lmx_status_str(lmx_status s) {
         case LMX_E_ALIGN: return "pointer misaligned for its layout";
         case LMX_E_LAUNCH: return "HIP launch failed";
         case LMX_E_DEVICE: return "no usable gfx950 device";
+        case LMX_E_FULL: return "no free sequence slot";
+        case LMX_E_HOST: return "host memory exhausted";
     }
     return "unknown status";
 }
 
-int lmx_version(void) { return 103; }
+int lmx_version(void) { return 104; }
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
     if (!ws) return LMX_E_NULL;
     if (!aligned(ws, 4) || ws_bytes % 4) return LMX_E_ALIGN;
-    const size_t n = ws_bytes / 4;
+    const bool quads = aligned(ws, 16) && ws_bytes % 16 == 0;
+    const size_t n = ws_bytes / (quads ? 16 : 4);
     size_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+    if (blocks > 8192) blocks = 8192;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(zero_words, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                       static_cast<uint32_t*>(ws), n);
+    if (quads)
+        hipLaunchKernelGGL(zero_quads, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           static_cast<uint4*>(ws), n);
+    else
+        hipLaunchKernelGGL(zero_words, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           static_cast<uint32_t*>(ws), n);
     LMX_CHECK_LAUNCH();
     return LMX_OK;
 }
