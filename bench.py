@@ -188,6 +188,24 @@ def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
     return {"t": t, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_matvec(lmx, torch, qtype, rows, in_dim, n_mats, steps=50, warmup=5):
+    """lmx_matvec at one token: y = W x over n_mats distinct weight matrices in
+    turn (so W comes from HBM, as a decode step's projections do).  Bytes are
+    the weight bytes (x and y are 4 * (in_dim + rows))."""
+    bb, be = {"q4_k": (144, 256), "q6_k": (210, 256), "q8_0": (34, 32), "bf16": (2, 1)}[qtype]
+    nbytes = rows * (in_dim // be) * bb
+    ws = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(n_mats)]
+    x = torch.randn((1, in_dim), device="cuda")
+    y = torch.empty((1, rows), device="cuda")
+    fns = [(lambda w=w: lmx.matvec(w, x, qtype=qtype, rows=rows, in_dim=in_dim, y=y)) for w in ws]
+    ms = time_calls(fns, steps, warmup, torch)
+    total = nbytes + 4 * (in_dim + rows)
+    gbs = total / (ms * 1e-3) / 1e9
+    del ws
+    return {"type": qtype, "rows": rows, "in_dim": in_dim, "weight_bytes": nbytes, "ms": ms,
+            "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def bench_kvm(lmx, torch, which, steps=20, warmup=3):
     """KV manager.  "wipe": zeroing one Qwen3-8B sequence slab (36 layers of
     f16 K and V at 32k positions, 4.83 GB) with lmx_kvm_wipe, an HBM write.
@@ -341,6 +359,10 @@ def main():
             ("delta_decode_1tok", lambda: bench_delta(lmx, torch, 1, False, steps=50, warmup=5)),
             ("delta_front_T4096", lambda: bench_delta_io(lmx, torch, 4096, "front")),
             ("delta_back_T4096", lambda: bench_delta_io(lmx, torch, 4096, "back")),
+            ("matvec_q4k_attn_output_4096", lambda: bench_matvec(lmx, torch, "q4_k", 4096, 4096, 36)),
+            ("matvec_q6k_lm_head_151936", lambda: bench_matvec(lmx, torch, "q6_k", 151936, 4096, 2, steps=20)),
+            ("matvec_q4k_ffn_up_12288", lambda: bench_matvec(lmx, torch, "q4_k", 12288, 4096, 36)),
+            ("matvec_q8_0_attn_output_4096", lambda: bench_matvec(lmx, torch, "q8_0", 4096, 4096, 36)),
             ("kvm_wipe_qwen3_8b_32k", lambda: bench_kvm(lmx, torch, "wipe")),
             ("kvm_batch_tables_b32", lambda: bench_kvm(lmx, torch, "batch")),
         ]:

@@ -302,6 +302,29 @@ lmx_status lmx_deltanet_back(const lmx_delta_back_desc *d, float *o, const float
                              const float *w, lmx_stream stream);
 
 /* ------------------------------------------------------------------------
+ * Quantized matrix-vector product: y[t] = W x[t], the attention epilogue's
+ * attn_output projection (qwen35.rs:1098-1109; forward.rs after attention) and
+ * any projection of the same form.  Replaces the reference's matvec_*
+ * dispatches (quant.wgsl:76-826) and computes what its CPU reference
+ * `dot_row` computes (crates/gguf/src/quant.rs:187-271).
+ *   W  rows x in_dim in ggml's on-disk row-major block layout: type 12 Q4_K
+ *      (144-byte blocks of 256), 14 Q6_K (210-byte blocks of 256, read in
+ *      place, no repacking), 8 Q8_0 (34-byte blocks of 32), 0 F32, 1 F16,
+ *      30 BF16; 16-byte aligned
+ *   x  [n_tok, in_dim] f32, y [n_tok, rows] f32, 16-byte aligned, disjoint
+ * in_dim: a multiple of 256 (Q4_K, Q6_K) or 64 (the others), at most 16384.
+ * Tokens go four per launch; each launch reads W once. */
+typedef struct {
+    uint32_t type;
+    uint32_t rows;
+    uint32_t in_dim;
+    uint32_t n_tok;
+} lmx_qmv_desc;
+
+lmx_status lmx_matvec(const lmx_qmv_desc *d, const void *w, const float *x, float *y,
+                      lmx_stream stream);
+
+/* ------------------------------------------------------------------------
  * Multi-sequence KV manager.  The reference serves one sequence at a time
  * (docs/limitations.md:21): one KvCache per session (cache.rs:65-154), sized
  * per layer as kv_slots (config.rs:279-284: min(window, n_ctx) ring slots for

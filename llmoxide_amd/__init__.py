@@ -147,6 +147,20 @@ class AttnExt(ctypes.Structure):
     ]
 
 
+class QmvDesc(ctypes.Structure):
+    """lmx_qmv_desc: a quantized (or dense) weight matrix times token vectors."""
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("rows", ctypes.c_uint32),
+        ("in_dim", ctypes.c_uint32),
+        ("n_tok", ctypes.c_uint32),
+    ]
+
+
+# ggml type codes lmx_matvec takes (crates/gguf: GgmlType)
+QTYPES = {"f32": 0, "f16": 1, "q8_0": 8, "q4_k": 12, "q6_k": 14, "bf16": 30}
+
+
 class KvmLayer(ctypes.Structure):
     """lmx_kvm_layer: one layer of a KV manager (window, row size, sharing)."""
     _fields_ = [
@@ -182,6 +196,7 @@ _PA, _PK, _PD = ctypes.POINTER(AttnParams), ctypes.POINTER(KvDesc), ctypes.POINT
 _PP = ctypes.POINTER(PrologueDesc)
 _PF, _PB = ctypes.POINTER(DeltaFrontDesc), ctypes.POINTER(DeltaBackDesc)
 _PX = ctypes.POINTER(AttnExt)
+_PQ = ctypes.POINTER(QmvDesc)
 _PKD, _PI32, _PU32 = ctypes.POINTER(KvmDesc), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_uint32)
 _PVP = ctypes.POINTER(ctypes.c_void_p)
 SIGNATURES = {
@@ -202,6 +217,7 @@ SIGNATURES = {
     "lmx_deltanet_recur": (ctypes.c_int, [_PD, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "lmx_deltanet_front": (ctypes.c_int, [_PF, _VP, _VP, _VP, _VP, _VP]),
     "lmx_deltanet_back": (ctypes.c_int, [_PB, _VP, _VP, _VP, _VP]),
+    "lmx_matvec": (ctypes.c_int, [_PQ, _VP, _VP, _VP, _VP]),
     "lmx_kvm_arena_bytes": (_SZ, [_PKD]),
     "lmx_kvm_create": (ctypes.c_int, [_PKD, _VP, _SZ, _PVP]),
     "lmx_kvm_destroy": (None, [_VP]),
@@ -506,6 +522,21 @@ def delta_back(o, z, w, *, n_vh: int, s_dim: int, eps: float = 1e-6, stream=None
     rc = lib().lmx_deltanet_back(ctypes.byref(d), _ptr(o), _ptr(z), _ptr(w), _stream(stream))
     _check("lmx_deltanet_back", rc)
     return o
+
+
+# ------------------------------------------------------ quantized matvec --
+def matvec(w, x, *, qtype, rows: int, in_dim: int, y=None, stream=None):
+    """y [n_tok, rows] = W x[t] for W in ggml's on-disk block layout (uint8
+    device tensor), x [n_tok, in_dim] f32 (quant.rs:187-271 ``dot_row``)."""
+    torch = _torch()
+    _need_cuda(w, x, y)
+    ty = QTYPES[qtype] if isinstance(qtype, str) else int(qtype)
+    n_tok = x.numel() // in_dim
+    if y is None:
+        y = torch.empty((n_tok, rows), dtype=torch.float32, device=x.device)
+    d = QmvDesc(ty, rows, in_dim, n_tok)
+    _check("lmx_matvec", lib().lmx_matvec(ctypes.byref(d), _ptr(w), _ptr(x), _ptr(y), _stream(stream)))
+    return y
 
 
 # --------------------------------------------------------------- KV manager --

@@ -24,6 +24,8 @@ bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt);
 lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
                        const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
                        float* out, hipStream_t st);
+// qmatvec.hip
+lmx_status qmatvec(const lmx_qmv_desc* d, const void* w, const float* x, float* y, hipStream_t st);
 // deltanet.hip
 lmx_status deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
                           const float* alpha, const float* beta, const float* conv, float* state,
@@ -145,7 +147,7 @@ const char* lmx_status_str(lmx_status s) {
     return "unknown status";
 }
 
-int lmx_version(void) { return 104; }
+int lmx_version(void) { return 105; }
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
@@ -391,6 +393,28 @@ lmx_status lmx_deltanet_back(const lmx_delta_back_desc* d, float* o, const float
     for (const void* p : {(const void*)o, (const void*)z, (const void*)w})
         if (!aligned(p, 4)) return LMX_E_ALIGN;
     return deltanet_back(d, o, z, w, (hipStream_t)stream);
+}
+
+lmx_status lmx_matvec(const lmx_qmv_desc* d, const void* w, const float* x, float* y,
+                      lmx_stream stream) {
+    if (!d || !w || !x || !y) return LMX_E_NULL;
+    if (d->rows == 0 || d->n_tok == 0 || d->in_dim == 0) return LMX_E_SHAPE;
+    uint32_t mult = 0;
+    size_t bb = 0, be = 1;
+    switch (d->type) {
+        case 12: mult = 256; bb = 144; be = 256; break;
+        case 14: mult = 256; bb = 210; be = 256; break;
+        case 8: mult = 64; bb = 34; be = 32; break;
+        case 0: mult = 64; bb = 4; break;
+        case 1: case 30: mult = 64; bb = 2; break;
+        default: return LMX_E_UNSUPPORTED;
+    }
+    if (d->in_dim % mult || d->in_dim > 16384) return LMX_E_SHAPE;
+    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 16)) return LMX_E_ALIGN;
+    const size_t wb = (size_t)d->rows * (d->in_dim / be) * bb;
+    const size_t xb = (size_t)d->n_tok * d->in_dim * 4, yb = (size_t)d->n_tok * d->rows * 4;
+    if (overlaps(y, yb, x, xb) || overlaps(y, yb, w, wb)) return LMX_E_SHAPE;
+    return qmatvec(d, w, x, y, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -113,6 +113,16 @@ def lib() -> ctypes.CDLL:
         L.orc_delta_front.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_float] + [f32p] * 4
         L.orc_delta_back.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_float] + [f32p] * 3
         L.orc_attn_gate.argtypes = [ctypes.c_int64] * 3 + [f32p] * 2
+        u8p = ctypes.POINTER(ctypes.c_uint8)
+        L.orc_block_bytes.argtypes = [ctypes.c_int]
+        L.orc_block_bytes.restype = ctypes.c_int64
+        L.orc_block_elems.argtypes = [ctypes.c_int]
+        L.orc_block_elems.restype = ctypes.c_int64
+        L.orc_dequant.argtypes = [ctypes.c_int, u8p, ctypes.c_int64, f32p]
+        L.orc_dot_row.argtypes = [ctypes.c_int, u8p, f32p, ctypes.c_int64]
+        L.orc_dot_row.restype = ctypes.c_float
+        L.orc_matvec.argtypes = [ctypes.c_int, u8p, ctypes.c_int64, ctypes.c_int64, f32p,
+                                 ctypes.c_int64, f32p]
         _lib = L
     return _lib
 
@@ -310,3 +320,76 @@ def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):
     t = o.size // (n_vh * s_dim)
     lib().orc_delta_back(t, n_vh, s_dim, eps, _f32p(o), _f32p(z), _f32p(w))
     return o
+
+
+# ------------------------------------------------------------- k-quants --
+# ggml type codes (GgmlType): the on-disk formats of crates/gguf/src/quant.rs.
+F32_T, F16_T, Q8_0, Q4_K, Q6_K, BF16_T = 0, 1, 8, 12, 14, 30
+QTYPES = {"f32": F32_T, "f16": F16_T, "q8_0": Q8_0, "q4_k": Q4_K, "q6_k": Q6_K, "bf16": BF16_T}
+
+
+def _u8p(a: np.ndarray):
+    assert a.dtype == np.uint8 and a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+
+
+def block_geometry(ty: int):
+    """(bytes, elements) per block of a type."""
+    return int(lib().orc_block_bytes(ty)), int(lib().orc_block_elems(ty))
+
+
+def row_bytes(ty: int, in_dim: int) -> int:
+    bb, be = block_geometry(ty)
+    assert in_dim % be == 0
+    return in_dim // be * bb
+
+
+def dequant(ty: int, data: np.ndarray, n: int) -> np.ndarray:
+    """quant.rs:130-182: n elements decoded to f32."""
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.zeros(n, np.float32)
+    lib().orc_dequant(ty, _u8p(data), n, _f32p(out))
+    return out
+
+
+def dot_row(ty: int, row: np.ndarray, x: np.ndarray) -> float:
+    """quant.rs:187-271: fused decode-and-dot of one row."""
+    row = np.ascontiguousarray(row, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    return float(lib().orc_dot_row(ty, _u8p(row), _f32p(x), x.size))
+
+
+def matvec(ty: int, w: np.ndarray, rows: int, in_dim: int, x: np.ndarray) -> np.ndarray:
+    """y[t, r] = dot_row(row r of w, x[t]); x [n_tok, in_dim]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, in_dim)
+    y = np.zeros((x.shape[0], rows), np.float32)
+    if lib().orc_matvec(ty, _u8p(w), rows, in_dim, _f32p(x), x.shape[0], _f32p(y)):
+        raise ValueError("orc_matvec: in_dim is not a whole number of blocks")
+    return y
+
+
+def quant_weights(ty: int, rows: int, in_dim: int, seed: int) -> np.ndarray:
+    """Random blocks of a type with scales in a sane range (the recipe of the
+    reference's quant.rs tests: patterned bytes, then f16 d (and dmin) set)."""
+    bb, be = block_geometry(ty)
+    n_blocks = rows * in_dim // be
+    if ty in (F32_T, F16_T, BF16_T):
+        vals = normal(seed, (rows * in_dim,)) * np.float32(0.05)
+        if ty == F32_T:
+            return vals.view(np.uint8).copy()
+        if ty == F16_T:
+            return to_f16_bits(vals).view(np.uint8).copy()
+        return (vals.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
+    raw = (uniform(seed, n_blocks * bb) * 256).astype(np.uint8).reshape(n_blocks, bb)
+    d = to_f16_bits(np.abs(normal(seed + 1, (n_blocks,))) * np.float32(0.01) + np.float32(0.001))
+    if ty == Q4_K:
+        raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        dm = to_f16_bits(np.abs(normal(seed + 2, (n_blocks,))) * np.float32(0.01))
+        raw[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    elif ty == Q6_K:
+        raw[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    else:  # Q8_0
+        raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    return np.ascontiguousarray(raw.reshape(-1))
+

@@ -44,6 +44,12 @@
  *                        q/k heads).
  *   orc_delta_back       crates/model/src/qwen35/cpu.rs:250-259 (gated RMS
  *                        norm), pinned by a float64 restatement.
+ *   orc_dequant / orc_dot_row / orc_matvec
+ *                        crates/gguf/src/quant.rs:33-260: ggml's Q4_K, Q6_K
+ *                        and Q8_0 blocks (on-disk layouts) and F32/F16/BF16
+ *                        rows, decoded and dotted in the reference's order;
+ *                        pinned by the reference's tests (quant.rs:301-415)
+ *                        and by a float64 decoder written from the layout.
  *   orc_attn_gate        crates/model/src/qwen35/cpu.rs:359-363 with
  *                        ops::sigmoid (ops.rs:181-183): the attention output
  *                        times sigmoid(gate); pinned by its special values
@@ -479,8 +485,6 @@ void orc_delta_front(int64_t n_tok, int64_t conv_dim, int64_t key_dim, int64_t s
     }
 }
 
-/* qwen35/cpu.rs:250-259: per token and v-head, rms_norm_mul(o, w) then
- * o *= silu(z), in place. */
 /* out[r][d] *= sigmoid(gate[r*gate_stride + d]) for r < n_rows, d < dim, in
  * the reference's order: sigmoid(x) = 1 / (1 + exp(-x)) in f32, then the
  * product (qwen35/cpu.rs:359-363, ops.rs:181-183). */
@@ -494,6 +498,8 @@ void orc_attn_gate(int64_t n_rows, int64_t dim, int64_t gate_stride, float *out,
         }
 }
 
+/* qwen35/cpu.rs:250-259: per token and v-head, rms_norm_mul(o, w) then
+ * o *= silu(z), in place. */
 void orc_delta_back(int64_t n_tok, int64_t n_vh, int64_t s_dim, float eps, float *o,
                     const float *z, const float *w) {
     for (int64_t r = 0; r < n_tok * n_vh; ++r) {
@@ -503,3 +509,193 @@ void orc_delta_back(int64_t n_tok, int64_t n_vh, int64_t s_dim, float eps, float
         for (int64_t j = 0; j < s_dim; ++j) oh[j] *= orc_silu(zh[j]);
     }
 }
+
+/* ------------------------------------------------------------ k-quants -- */
+/* Type codes (ggml's GgmlType numbering): F32 0, F16 1, Q8_0 8, Q4_K 12,
+ * Q6_K 14, BF16 30. */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4K = 12, ORC_Q6K = 14, ORC_BF16 = 30 };
+
+static float orc_le_f16(const uint8_t *b) { return orc_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))); }
+
+static float orc_le_bf16(const uint8_t *b) {
+    uint32_t u = (uint32_t)(b[0] | (b[1] << 8)) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* quant.rs:33-47 */
+static void orc_q4k_scale_min(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* Bytes per block and elements per block of a type (0 for an unknown type). */
+int64_t orc_block_bytes(int ty) {
+    switch (ty) {
+        case ORC_F32: return 4;
+        case ORC_F16: case ORC_BF16: return 2;
+        case ORC_Q8_0: return 34;
+        case ORC_Q4K: return 144;
+        case ORC_Q6K: return 210;
+        default: return 0;
+    }
+}
+int64_t orc_block_elems(int ty) {
+    switch (ty) {
+        case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
+        case ORC_Q8_0: return 32;
+        case ORC_Q4K: case ORC_Q6K: return 256;
+        default: return 0;
+    }
+}
+
+/* quant.rs:54-128, 130-182: n elements (a multiple of the block size). */
+void orc_dequant(int ty, const uint8_t *data, int64_t n, float *out) {
+    if (ty == ORC_F32) { memcpy(out, data, (size_t)n * 4); return; }
+    if (ty == ORC_F16) { for (int64_t i = 0; i < n; ++i) out[i] = orc_le_f16(data + 2 * i); return; }
+    if (ty == ORC_BF16) { for (int64_t i = 0; i < n; ++i) out[i] = orc_le_bf16(data + 2 * i); return; }
+    if (ty == ORC_Q8_0) {
+        for (int64_t b = 0; b < n / 32; ++b) {
+            const uint8_t *blk = data + b * 34;
+            const float d = orc_le_f16(blk);
+            for (int i = 0; i < 32; ++i) out[b * 32 + i] = d * (float)(int8_t)blk[2 + i];
+        }
+        return;
+    }
+    if (ty == ORC_Q4K) {
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const uint8_t *blk = data + b * 144;
+            const float d = orc_le_f16(blk), dmin = orc_le_f16(blk + 2);
+            const uint8_t *sc = blk + 4, *qs = blk + 16;
+            float *o = out + b * 256;
+            for (int pair = 0; pair < 4; ++pair) {
+                uint8_t sc1, m1, sc2, m2;
+                orc_q4k_scale_min(pair * 2, sc, &sc1, &m1);
+                orc_q4k_scale_min(pair * 2 + 1, sc, &sc2, &m2);
+                const float d1 = d * (float)sc1, min1 = dmin * (float)m1;
+                const float d2 = d * (float)sc2, min2 = dmin * (float)m2;
+                const uint8_t *q = qs + pair * 32;
+                for (int l = 0; l < 32; ++l) {
+                    o[pair * 64 + l] = d1 * (float)(q[l] & 0xF) - min1;
+                    o[pair * 64 + l + 32] = d2 * (float)(q[l] >> 4) - min2;
+                }
+            }
+        }
+        return;
+    }
+    if (ty == ORC_Q6K) {
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const uint8_t *blk = data + b * 210;
+            const float d = orc_le_f16(blk + 208);
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
+                const int8_t *sc = (const int8_t *)(blk + 192 + h * 8);
+                float *y = out + b * 256 + h * 128;
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const uint8_t hb = qh[l];
+                    const int q1 = ((ql[l] & 0xF) | ((hb & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0xF) | (((hb >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((hb >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((hb >> 6) & 3) << 4)) - 32;
+                    y[l] = d * (float)sc[is] * (float)q1;
+                    y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                    y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                    y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                }
+            }
+        }
+    }
+}
+
+/* quant.rs:187-271: the fused decode-and-dot of one row with x[n]. */
+float orc_dot_row(int ty, const uint8_t *row, const float *x, int64_t n) {
+    float acc = 0.f;
+    if (ty == ORC_Q4K) {
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const uint8_t *blk = row + b * 144;
+            const float d = orc_le_f16(blk), dmin = orc_le_f16(blk + 2);
+            const uint8_t *sc = blk + 4, *qs = blk + 16;
+            const float *xb = x + b * 256;
+            for (int pair = 0; pair < 4; ++pair) {
+                uint8_t sc1, m1, sc2, m2;
+                orc_q4k_scale_min(pair * 2, sc, &sc1, &m1);
+                orc_q4k_scale_min(pair * 2 + 1, sc, &sc2, &m2);
+                const uint8_t *q = qs + pair * 32;
+                const float *xl = xb + pair * 64;
+                float s1 = 0.f, x1 = 0.f, s2 = 0.f, x2 = 0.f;
+                for (int l = 0; l < 32; ++l) {
+                    const float a = xl[l], c = xl[l + 32];
+                    s1 += (float)(q[l] & 0xF) * a;
+                    x1 += a;
+                    s2 += (float)(q[l] >> 4) * c;
+                    x2 += c;
+                }
+                acc += d * (float)sc1 * s1 - dmin * (float)m1 * x1;
+                acc += d * (float)sc2 * s2 - dmin * (float)m2 * x2;
+            }
+        }
+        return acc;
+    }
+    if (ty == ORC_Q6K) {
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const uint8_t *blk = row + b * 210;
+            const float d = orc_le_f16(blk + 208);
+            const float *xb = x + b * 256;
+            float sub = 0.f;
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
+                const int8_t *sc = (const int8_t *)(blk + 192 + h * 8);
+                const float *y = xb + h * 128;
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const uint8_t hb = qh[l];
+                    const int q1 = ((ql[l] & 0xF) | ((hb & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0xF) | (((hb >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((hb >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((hb >> 6) & 3) << 4)) - 32;
+                    sub += (float)sc[is] * (float)q1 * y[l] + (float)sc[is + 2] * (float)q2 * y[l + 32] +
+                           (float)sc[is + 4] * (float)q3 * y[l + 64] + (float)sc[is + 6] * (float)q4 * y[l + 96];
+                }
+            }
+            acc += d * sub;
+        }
+        return acc;
+    }
+    if (ty == ORC_Q8_0) {
+        for (int64_t b = 0; b < n / 32; ++b) {
+            const uint8_t *blk = row + b * 34;
+            const float d = orc_le_f16(blk);
+            float sub = 0.f;
+            for (int i = 0; i < 32; ++i) sub += (float)(int8_t)blk[2 + i] * x[b * 32 + i];
+            acc += d * sub;
+        }
+        return acc;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        const float w = ty == ORC_F32 ? ((const float *)row)[i]
+                      : ty == ORC_F16 ? orc_le_f16(row + 2 * i) : orc_le_bf16(row + 2 * i);
+        acc += w * x[i];
+    }
+    return acc;
+}
+
+/* y[t][r] = dot_row(row r of w, x[t]) for t < n_tok, r < rows: what the
+ * reference's matvec kernels compute and are checked against. */
+int orc_matvec(int ty, const uint8_t *w, int64_t rows, int64_t in_dim, const float *x,
+               int64_t n_tok, float *y) {
+    const int64_t bb = orc_block_bytes(ty), be = orc_block_elems(ty);
+    if (!bb || in_dim % be) return 1;
+    const int64_t row_bytes = in_dim / be * bb;
+    for (int64_t t = 0; t < n_tok; ++t)
+        for (int64_t r = 0; r < rows; ++r)
+            y[t * rows + r] = orc_dot_row(ty, w + r * row_bytes, x + t * in_dim, in_dim);
+    return 0;
+}
+

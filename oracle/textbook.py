@@ -216,3 +216,56 @@ def delta_back(o, z, w, *, n_vh, s_dim, eps=1e-6):
     z = np.asarray(z, np.float64).reshape(o.shape)
     o = o / np.sqrt((o * o).mean(-1, keepdims=True) + eps) * np.asarray(w, np.float64)
     return (o * (z / (1.0 + np.exp(-z)))).reshape(o.shape[0], -1)
+
+
+# ------------------------------------------------------------- k-quants --
+def _f16(lo, hi):
+    return np.frombuffer(np.stack([lo, hi], -1).astype(np.uint8).tobytes(), np.float16).astype(np.float64)
+
+
+def dequant(ty, data, n):
+    """ggml's block layouts decoded in float64, vectorized over blocks (a
+    second, independent reading of the formats quant.rs:12-128 describes)."""
+    data = np.asarray(data, np.uint8)
+    if ty == 0:
+        return np.frombuffer(data.tobytes(), np.float32)[:n].astype(np.float64)
+    if ty == 1:
+        return np.frombuffer(data.tobytes(), np.float16)[:n].astype(np.float64)
+    if ty == 30:
+        u = np.frombuffer(data.tobytes(), np.uint16)[:n].astype(np.uint32) << 16
+        return u.view(np.float32).astype(np.float64)
+    if ty == 8:  # Q8_0: f16 d, 32 x i8
+        b = data.reshape(-1, 34)
+        d = _f16(b[:, 0], b[:, 1])
+        q = b[:, 2:].view(np.int8).astype(np.float64)
+        return (d[:, None] * q).reshape(-1)[:n]
+    if ty == 12:  # Q4_K: f16 d, f16 dmin, 12 bytes of 6-bit (scale, min), 128 nibble bytes
+        b = data.reshape(-1, 144)
+        d, dmin = _f16(b[:, 0], b[:, 1]), _f16(b[:, 2], b[:, 3])
+        q = b[:, 4:16].astype(np.int64)
+        sc = np.zeros((b.shape[0], 8), np.int64)
+        mn = np.zeros((b.shape[0], 8), np.int64)
+        sc[:, :4], mn[:, :4] = q[:, 0:4] & 63, q[:, 4:8] & 63
+        sc[:, 4:] = (q[:, 8:12] & 15) | ((q[:, 0:4] >> 6) << 4)
+        mn[:, 4:] = (q[:, 8:12] >> 4) | ((q[:, 4:8] >> 6) << 4)
+        nib = b[:, 16:].reshape(-1, 4, 32).astype(np.int64)
+        vals = np.stack([nib & 15, nib >> 4], 2).reshape(-1, 8, 32)  # sub-block 2p low, 2p+1 high
+        out = d[:, None, None] * sc[:, :, None] * vals - dmin[:, None, None] * mn[:, :, None]
+        return out.reshape(-1)[:n]
+    if ty == 14:  # Q6_K: 128 low-nibble bytes, 64 high-bit bytes, 16 i8 scales, f16 d
+        b = data.reshape(-1, 210)
+        d = _f16(b[:, 208], b[:, 209])
+        scales = b[:, 192:208].view(np.int8).astype(np.int64)
+        out = np.zeros((b.shape[0], 256))
+        for h in range(2):
+            ql = b[:, h * 64:h * 64 + 64].astype(np.int64)
+            qh = b[:, 128 + h * 32:128 + h * 32 + 32].astype(np.int64)
+            for g in range(4):  # element 128h + 32g + l
+                low = (ql[:, :32] if g % 2 == 0 else ql[:, 32:])
+                low = (low & 15) if g < 2 else (low >> 4)
+                q = (low | (((qh >> (2 * g)) & 3) << 4)) - 32
+                s = scales[:, 8 * h + 2 * g + (np.arange(32) // 16)]
+                out[:, 128 * h + 32 * g:128 * h + 32 * g + 32] = d[:, None] * s * q
+        return out.reshape(-1)[:n]
+    raise ValueError(ty)
+

@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 28
+    assert len(names) == 29
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = lmx.lib()
-    assert L.lmx_version() == 104
+    assert L.lmx_version() == 105
     for s in lmx.Status:
         assert L.lmx_status_str(int(s))
     assert L.lmx_status_str(999) == b"unknown status"
@@ -236,3 +236,20 @@ def test_delta_front_back_validation():
     assert back(n_tok=0) == lmx.Status.E_SHAPE
     assert back(o=None) == lmx.Status.E_NULL
     assert back(o=FAKE + 1) == lmx.Status.E_ALIGN
+
+
+def _mv(ty=12, rows=8, in_dim=512, n_tok=1, w=FAKE, x=FAKE + (1 << 24), y=FAKE + (1 << 25)):
+    d = lmx.QmvDesc(ty, rows, in_dim, n_tok)
+    return lmx.lib().lmx_matvec(ctypes.byref(d), w, x, y, None)
+
+
+def test_matvec_validates_before_launching():
+    assert _mv(w=None) == lmx.Status.E_NULL
+    assert _mv(ty=2) == lmx.Status.E_UNSUPPORTED          # Q4_0: not a path type
+    assert _mv(ty=12, in_dim=320) == lmx.Status.E_SHAPE   # not a whole number of 256-blocks
+    assert _mv(ty=8, in_dim=96) == lmx.Status.E_SHAPE     # Q8_0 units are 64 wide
+    assert _mv(in_dim=16384 + 256) == lmx.Status.E_SHAPE
+    assert _mv(rows=0) == lmx.Status.E_SHAPE
+    assert _mv(w=FAKE + 8) == lmx.Status.E_ALIGN
+    assert _mv(y=FAKE + (1 << 24) + 64) == lmx.Status.E_SHAPE  # y over x
+

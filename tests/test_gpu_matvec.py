@@ -1,0 +1,61 @@
+"""GPU parity of lmx_matvec against the oracle's `dot_row` restatement
+(crates/gguf/src/quant.rs:187-271) for every block format the path takes.
+
+Tolerance: max|y - ref| <= 3e-5 * max|ref|: both sum thousands of f32
+products, in different orders (the oracle per 32-element sub-block as the
+reference does, the GPU per lane then across lanes)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import llmoxide_amd as lmx  # noqa: E402
+
+TYPES = ["q4_k", "q6_k", "q8_0", "f32", "f16", "bf16"]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run(name, rows, in_dim, n_tok, seed):
+    say(f"matvec {name} rows={rows} in_dim={in_dim} n_tok={n_tok}")
+    ty = oracle.QTYPES[name]
+    w = oracle.quant_weights(ty, rows, in_dim, seed)
+    x = oracle.normal(seed + 50, (n_tok, in_dim))
+    ref = oracle.matvec(ty, w, rows, in_dim, x)
+    y = lmx.matvec(torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(), qtype=name, rows=rows,
+                   in_dim=in_dim)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    err = np.abs(got - ref).max()
+    assert err <= 3e-5 * np.abs(ref).max(), f"{name}: max err {err} vs max |ref| {np.abs(ref).max()}"
+
+
+@pytest.mark.parametrize("name", TYPES)
+def test_attn_output_shape_decode(name):
+    # Qwen3-8B attn_output: 4096 x 4096, one token
+    run(name, 4096, 4096, 1, seed=1)
+
+
+@pytest.mark.parametrize("name", TYPES)
+@pytest.mark.parametrize("n_tok", [2, 4, 7])
+def test_ragged_rows_and_token_tiles(name, n_tok):
+    # rows not a multiple of the 16 a workgroup takes; 7 tokens = two launches
+    run(name, 37, 512, n_tok, seed=2 + n_tok)
+
+
+@pytest.mark.parametrize("name", ["q4_k", "q6_k", "q8_0"])
+def test_widest_rows(name):
+    run(name, 64, 16384, 1, seed=9)
+
+
+def test_odd_q6k_block_count_per_row():
+    # 3 blocks per row: half the blocks start 2 bytes past a dword boundary
+    run("q6_k", 33, 768, 2, seed=10)
