@@ -246,12 +246,15 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         const f16* Ks = K_s + stage * (BN * KPAD);
         const f16* Vts = Vt_s + stage * (HD * VPAD);
 
-        // ---- S^T = K Q^T, two 32-key blocks
+        // ---- S^T - m = K Q^T - m, two 32-key blocks.  The accumulators start
+        //      at -mb (mb = the running max once one is set), so the scores
+        //      come out already shifted for exp2.
+        const float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
+            for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
             const f16* krow = &Ks[(kb * 32 + l32) * KPAD + 8 * hh];
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -275,10 +278,12 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
                 s[kb][i] = x;
                 mt = fmaxf(mt, x);
             }
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the tile's largest score
         // Lazy rescale: the running max moves only when some lane's tile max
         // exceeds it by more than kRescaleSlack (log2 units), so most tiles
         // skip the o *= corr pass; p = exp2(x - m_run) stays <= 2^slack.
+        // Off that path mb == m_run (or the tile is fully masked), so s
+        // already holds x - m_run.
         if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack) != 0) {
             const float mn = fmaxf(m_run, mt);
             const float corr = fast_exp2(m_run - mn);
@@ -288,6 +293,11 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+            const float shift = mn - mb;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[kb][i] -= shift;
         }
 
         // P^T as the B operand of PST k-steps (16 keys each): step st takes
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
         for (int st = 0; st < PST; ++st) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j] - m_run);
+            for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j]);
 #pragma unroll
             for (int j = 0; j < 8; j += 2)
                 l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
