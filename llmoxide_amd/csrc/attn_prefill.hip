@@ -144,7 +144,11 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 
     // ---- K/V tiles: global -> registers (the next tile's loads are in
     // flight while the current tile is computed) -> one of two LDS stages.
-    // Rows outside [wg_lo, wg_hi] are zero.
+    // Rows outside [wg_lo, wg_hi] are zero.  V is stored transposed; its
+    // copy gives consecutive lanes consecutive 4-key groups (kg) of one 8-dim
+    // chunk (dc), so the 8-byte transposed stores of 16 lanes fill all 32
+    // banks once.  Consecutive dims would put lanes 8 rows apart, on two
+    // banks (the row stride is 16 banks mod 32).
     constexpr int KCH = HD / 8;                   // 16-byte chunks per key row
     constexpr int KPT = BN * KCH / 256;           // K chunks per thread
     constexpr int VPT = (KCH * (BN / 4) + 255) / 256;  // V 4-key groups per thread
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int pr = tid + 256 * i;
-            const int dc = pr % KCH, kg = pr / KCH;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
             if (pr < KCH * (BN / 4))
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
@@ -200,7 +204,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int pr = tid + 256 * i;
-            const int dc = pr % KCH, kg = pr / KCH;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int p = kt + 4 * kg + u;
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         for (int i = 0; i < VPT; ++i) {
             const int pr = tid + 256 * i;
             if (pr >= KCH * (BN / 4)) continue;
-            const int dc = pr % KCH, kg = pr / KCH;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 *reinterpret_cast<f16x4*>(&Vts[(dc * 8 + j) * VPAD + 4 * kg]) =
