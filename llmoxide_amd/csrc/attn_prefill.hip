@@ -267,28 +267,49 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             }
         }
 
-        // ---- scale, mask, online softmax.  s[kb][i] is key
-        //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow.
-        float mt = -INFINITY;
+        // ---- mask, online softmax.  s[kb][i] is key
+        //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
+        if (need_mask) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+            for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float x = s[kb][i];
-                if (need_mask) {
+                for (int i = 0; i < 16; ++i) {
                     const int key = kt + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
-                    if (key < my_lo || key > my_hi) x = -INFINITY;
+                    if (key < my_lo || key > my_hi) s[kb][i] = -INFINITY;
                 }
-                s[kb][i] = x;
-                mt = fmaxf(mt, x);
-            }
-        mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the tile's largest score
-        // Lazy rescale: the running max moves only when some lane's tile max
-        // exceeds it by more than kRescaleSlack (log2 units), so most tiles
-        // skip the o *= corr pass; p = exp2(x - m_run) stays <= 2^slack.
-        // Off that path mb == m_run (or the tile is fully masked), so s
-        // already holds x - m_run.
-        if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack) != 0) {
+        }
+        // P^T as the B operand of PST k-steps (16 keys each): step st takes
+        // registers 8*(st%2) .. +7 of s[st/2].  p = exp2(s) is formed first;
+        // the lazy rescale then only asks whether some p exceeds 2^slack
+        // (a score above m_run + slack), which a packed f16 max over the
+        // rounded p answers with a quarter of the instructions of a float
+        // max over the scores.  That tile, and a query's first tile (m_run
+        // not set yet), take the exact path: the float max, the rescale of
+        // o and l, and p again.
+        f16x8 pf[PST];
+        auto make_p = [&]() {
+#pragma unroll
+            for (int st = 0; st < PST; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j]);
+        };
+        make_p();
+        f16x2 pm = {pf[0][0], pf[0][1]};
+#pragma unroll
+        for (int st = 0; st < PST; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{pf[st][j], pf[st][j + 1]});
+        float pmax = fmaxf((float)pm[0], (float)pm[1]);
+        pmax = fmaxf(pmax, shfl_xor(pmax, 32));
+        constexpr float kSlackP = 256.f;  // 2^kRescaleSlack
+        static_assert(kRescaleSlack == 8.f, "kSlackP is 2^kRescaleSlack");
+        if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kb][i]);
+            mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the tile's largest score
             const float mn = fmaxf(m_run, mt);
             const float corr = fast_exp2(m_run - mn);
             m_run = mn;
@@ -302,22 +323,17 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) s[kb][i] -= shift;
+            make_p();
         }
 
-        // P^T as the B operand of PST k-steps (16 keys each): step st takes
-        // registers 8*(st%2) .. +7 of s[st/2].
         // The row sum takes the f16-rounded p, as the P.V product does, two
         // at a time (v_dot2_f32_f16 against 1).
-        f16x8 pf[PST];
         const f16x2 one2 = {(f16)1.f, (f16)1.f};
 #pragma unroll
-        for (int st = 0; st < PST; ++st) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j]);
+        for (int st = 0; st < PST; ++st)
 #pragma unroll
             for (int j = 0; j < 8; j += 2)
                 l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
-        }
 
         // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
         //      16*st' + 4*hh + {0..3} and 16*st' + 8 + 4*hh + {0..3} of the tile.
