@@ -253,7 +253,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         // ---- S^T - m = K Q^T - m, two 32-key blocks.  The accumulators start
         //      at -mb (mb = the running max once one is set), so the scores
         //      come out already shifted for exp2.
-        const float mb = m_run > -1e29f ? m_run : 0.f;
+        float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -278,74 +278,81 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
                     if (key < my_lo || key > my_hi) s[kb][i] = -INFINITY;
                 }
         }
-        // P^T as the B operand of PST k-steps (16 keys each): step st takes
-        // registers 8*(st%2) .. +7 of s[st/2].  p = exp2(s) is formed first;
-        // the lazy rescale then only asks whether some p exceeds 2^slack
-        // (a score above m_run + slack), which a packed f16 max over the
-        // rounded p answers with a quarter of the instructions of a float
-        // max over the scores.  That tile, and a query's first tile (m_run
-        // not set yet), take the exact path: the float max, the rescale of
-        // o and l, and p again.
-        f16x8 pf[PST];
-        auto make_p = [&]() {
-#pragma unroll
-            for (int st = 0; st < PST; ++st)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j]);
-        };
-        make_p();
-        f16x2 pm = {pf[0][0], pf[0][1]};
-#pragma unroll
-        for (int st = 0; st < PST; ++st)
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{pf[st][j], pf[st][j + 1]});
-        float pmax = fmaxf((float)pm[0], (float)pm[1]);
-        pmax = fmaxf(pmax, shfl_xor(pmax, 32));
+        // The tile in two halves of 32 keys (kb), each with its own softmax
+        // step, so that the P.V MFMAs of half 0 can run while half 1's p is
+        // formed.  P^T of a half is the B operand of two 16-key k-steps,
+        // registers 0..7 and 8..15 of s[kb].  p = exp2(s) is formed first; the
+        // lazy rescale then only asks whether some p exceeds 2^slack (a score
+        // above m_run + slack), which a packed f16 max over the rounded p
+        // answers with a quarter of the instructions of a float max over the
+        // scores.  Such a half, and a query's first one (m_run not set yet),
+        // take the exact path: the float max, the rescale of o and l, and p
+        // again.
         constexpr float kSlackP = 256.f;  // 2^kRescaleSlack
         static_assert(kRescaleSlack == 8.f, "kSlackP is 2^kRescaleSlack");
-        if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
-            float mt = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kb][i]);
-            mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the tile's largest score
-            const float mn = fmaxf(m_run, mt);
-            const float corr = fast_exp2(m_run - mn);
-            m_run = mn;
-            l_run *= corr;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
-            const float shift = mn - mb;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s[kb][i] -= shift;
-            make_p();
-        }
-
-        // The row sum takes the f16-rounded p, as the P.V product does, two
-        // at a time (v_dot2_f32_f16 against 1).
         const f16x2 one2 = {(f16)1.f, (f16)1.f};
 #pragma unroll
-        for (int st = 0; st < PST; ++st)
+        for (int kb = 0; kb < KB; ++kb) {
+            f16x8 pf[2];
+            auto make_p = [&]() {
 #pragma unroll
-            for (int j = 0; j < 8; j += 2)
-                l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[kb][8 * st + j]);
+            };
+            make_p();
+            f16x2 pm = {pf[0][0], pf[0][1]};
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{pf[st][j], pf[st][j + 1]});
+            float pmax = fmaxf((float)pm[0], (float)pm[1]);
+            pmax = fmaxf(pmax, shfl_xor(pmax, 32));
+            if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
+                float mt = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kb][i]);
+                mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the half's largest score
+                const float mn = fmaxf(m_run, mt);
+                const float corr = fast_exp2(m_run - mn);
+                m_run = mn;
+                l_run *= corr;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+                // The scores still to come in this tile become relative to
+                // mn; while a query has seen no key (a masked half, m_run
+                // still unset) they stay relative to 0.
+                const float nmb = mn > -1e29f ? mn : 0.f;
+                const float shift = nmb - mb;
+#pragma unroll
+                for (int k2 = kb; k2 < KB; ++k2)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[k2][i] -= shift;
+                mb = nmb;
+                make_p();
+            }
+            // The row sum takes the f16-rounded p, as the P.V product does,
+            // two at a time (v_dot2_f32_f16 against 1).
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2)
+                    l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
 
-        // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
-        //      16*st' + 4*hh + {0..3} and 16*st' + 8 + 4*hh + {0..3} of the tile.
+            // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
+            //      32*kb + 16*st + 4*hh + {0..3} and + 8 + 4*hh + {0..3}.
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 4 * hh];
+            for (int nb = 0; nb < NB; ++nb) {
+                const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 32 * kb + 4 * hh];
 #pragma unroll
-            for (int st = 0; st < PST; ++st) {
-                const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
-                const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
-                const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[st], o[nb], 0, 0, 0);
+                for (int st = 0; st < 2; ++st) {
+                    const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
+                    const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
+                    const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[st], o[nb], 0, 0, 0);
+                }
             }
         }
     }
