@@ -11,12 +11,18 @@
 //                 S^T accumulators (no shuffle: computing the transpose makes
 //                 each lane own one query column, so softmax is mostly in-lane)
 //
-// Workgroup = 4 waves x 32 query rows of one query head; K/V tiles of 64 keys
-// are staged in LDS.  Key tiles outside a wave's visible range are skipped
-// (causal / window), tiles inside every query's range skip the mask.
-// Workgroups are ordered so each XCD owns whole kv heads (its L2 serves the
-// G query heads that share them) and heavy causal tiles start first.
+// Two kernels share these tiles.  attn_prefill_kernel: workgroup = 4 waves x
+// 32 query rows of one query head, two workgroups per CU.  The ping-pong
+// kernel (head_dim 128, long batches): 8 waves x 32 rows, one workgroup per
+// CU, the two waves of each SIMD kept half a tile apart so one's MFMAs run
+// beside the other's softmax.  K/V tiles of 64 keys are staged in LDS.  Key
+// tiles outside a wave's visible range are skipped (causal / window), tiles
+// inside every query's range skip the mask.  Workgroups are ordered so each
+// XCD owns whole kv heads (its L2 serves the G query heads that share them)
+// and heavy causal tiles start first.
 #include <climits>
+#include <cstdlib>
+#include <cstring>
 
 #include "common.hpp"
 
@@ -306,8 +312,9 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             for (int st = 0; st < 2; ++st)
 #pragma unroll
                 for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{pf[st][j], pf[st][j + 1]});
-            float pmax = fmaxf((float)pm[0], (float)pm[1]);
-            pmax = fmaxf(pmax, shfl_xor(pmax, 32));
+            // The test is "some p of the wave exceeds 2^slack": a ballot over
+            // each lane's own p, no combine of a query's two half-columns.
+            const float pmax = fmaxf((float)pm[0], (float)pm[1]);
             if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
                 float mt = -INFINITY;
 #pragma unroll
@@ -375,6 +382,390 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         }
 }
 
+// ---- Ping-pong variant (head_dim <= 128) -----------------------------------
+//
+// Eight waves, two per SIMD, each owning 32 query rows of a 256-row block
+// (the same S^T = K Q^T, O^T += V^T P^T tiles as above).  A wave's work on key
+// tile i is split into an MFMA phase, QK(i) and PV(i-1), and a VALU phase,
+// mask + softmax(i) plus a share of the K/V copy.  Two barriers per tile keep
+// group 0 (waves 0-3) and group 1 (waves 4-7) a phase apart, so on each SIMD
+// one wave's MFMAs run while the other wave's exponentials issue:
+//
+//              phase 1                      phase 2
+//   group 0    QK(i), PV(i-1)               softmax(i), copy K(i+1)
+//   group 1    softmax(i-1), copy V(i)      QK(i), PV(i-1)
+//
+// K tile i and V tile i-1 are read in iteration i; the stages written in
+// iteration i (K(i+1), V(i)) were last read in iteration i-1.  The MFMA
+// phase runs at wave priority 1, so the SIMD issues the next MFMA as soon as
+// the matrix pipe takes it and fills the gaps with the other wave's VALU.
+constexpr int kPpBM = 256;  // query rows per workgroup: 8 waves x 32
+
+template <typename QT, int HD>
+__global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) {
+    constexpr int BN = 64;
+    constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
+    constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
+    constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
+    constexpr int NB = HD / 32;      // 32-dim output blocks
+    constexpr int KPAD = HD + 8;
+    constexpr int VPAD = BN + 4;
+    static_assert(HD <= 128, "two waves per SIMD");
+    __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
+
+    const int nblk = gridDim.x;
+    const int logical = xcd_remap(blockIdx.x, nblk);
+    const int per_kvh = a.n_qtiles * a.G;
+    const int kvh = logical / per_kvh;
+    const int rem = logical - kvh * per_kvh;
+    const int qt = a.n_qtiles - 1 - rem / a.G;
+    const int h = kvh * a.G + (rem % a.G);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int ctid = tid & 255;  // thread index within the group (the copy split)
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int t = a.n_tokens, base = a.base_pos, w = a.window;
+    const int end = base + t - 1;
+    const int q0 = qt * kPpBM;
+    // The groups take alternate 32-row blocks, so the two waves of a SIMD
+    // have nearly the same causal key range.
+    const int qw0 = q0 + 32 * (2 * (wave & 3) + grp);
+
+    const int qrow = qw0 + l32;
+    const bool qvalid = qrow < t;
+    const int qpos = base + qrow;
+    const int my_lo = qvalid ? vis_lo(qpos, w) : 1;
+    const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
+
+    f16x8 qf[KSTEPS];
+    {
+        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            float x[8];
+            if constexpr (sizeof(QT) == 2) {
+                const f16x8 q8 = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qoff + ks * 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = (float)q8[j];
+            } else {
+                const float* qp = reinterpret_cast<const float*>(a.q) + qoff + ks * 16;
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[j] = x0[j];
+                    x[4 + j] = x1[j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(x[j] * a.c);
+        }
+    }
+
+    // ---- key tiles of the workgroup, and the wave's own run of them
+    const int q_last = min(q0 + kPpBM, t) - 1;
+    const int wg_lo = vis_lo(base + q0, w);
+    const int wg_hi = vis_hi(base + q_last, w, a.bidi, end);
+    const int kt_begin = (wg_lo / BN) * BN;
+    const int n_t = wg_lo <= wg_hi ? (wg_hi - kt_begin) / BN + 1 : 0;
+    const bool wave_live = qw0 < t;
+    const int wq_last = min(qw0 + 31, t - 1);
+    const int wv_lo_max = wave_live ? vis_lo(base + wq_last, w) : 0;           // largest lo
+    const int wv_hi_min = wave_live ? vis_hi(base + qw0, w, a.bidi, end) : -1;  // smallest hi
+    int wi0 = 1, wi1 = 0;  // empty
+    if (wave_live) {
+        const int wv_lo = vis_lo(base + qw0, w);
+        const int wv_hi = min(vis_hi(base + wq_last, w, a.bidi, end), wg_hi);
+        if (wv_lo <= wv_hi) {
+            wi0 = (wv_lo - kt_begin) / BN;
+            wi1 = (wv_hi - kt_begin) / BN;
+        }
+    }
+    const int cur_begin = a.k_cur ? base : INT_MAX;
+
+    float m_run = -1e30f, l_run = 0.f, mb = 0.f;
+    f32x16 o[NB];
+    f32x16 s[KB];
+    f16x8 P[PST];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[nb][i] = 0.f;
+
+    // ---- K/V copies, as in the kernel above; group 0 copies K, group 1 V,
+    //      each with its 256 threads (ctid).
+    constexpr int KCH = HD / 8;
+    constexpr int KPT = BN * KCH / 256;
+    constexpr int VPT = (KCH * (BN / 4) + 255) / 256;
+    static_assert(BN * KCH % 256 == 0, "K tile split");
+    f16x8 rk[KPT];
+    f16x8 rv[VPT][4];
+    auto row_src = [&](const f16* cache, const f16* cur, int p) -> const f16* {
+        if (p >= cur_begin) return cur + (size_t)(p - base) * a.kv_dim;
+        const int sl = w ? p % w : p;
+        return cache + (size_t)sl * a.kv_dim;
+    };
+    // The consecutive-slot base of a tile whose rows are all visible to the
+    // workgroup and come from the cache, else NULL.
+    auto fast_base = [&](const f16* cache, int kt) -> const f16* {
+        if (kt < wg_lo || kt + BN - 1 > wg_hi || kt + BN - 1 >= cur_begin) return nullptr;
+        int s0 = kt;
+        if (w) {
+            s0 = kt % w;
+            if (s0 + BN > w) return nullptr;
+        }
+        return cache + (size_t)s0 * a.kv_dim + kvh * HD;
+    };
+    auto fetch_k = [&](int kt) {
+        if (const f16* kb = fast_base(a.k, kt)) {
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                const int c = ctid + 256 * i;
+                const int key = c / KCH, col = c - key * KCH;
+                rk[i] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * a.kv_dim + col * 8);
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = ctid + 256 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            const int p = kt + key;
+            f16x8 val = {};
+            if (p >= wg_lo && p <= wg_hi)
+                val = *reinterpret_cast<const f16x8*>(row_src(a.k, a.k_cur, p) + kvh * HD + col * 8);
+            rk[i] = val;
+        }
+    };
+    auto fetch_v = [&](int kt) {
+        if (const f16* vb = fast_base(a.v, kt)) {
+#pragma unroll
+            for (int i = 0; i < VPT; ++i) {
+                const int pr = ctid + 256 * i;
+                const int kg = pr % (BN / 4), dc = pr / (BN / 4);
+                if (pr < KCH * (BN / 4))
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        rv[i][u] = *reinterpret_cast<const f16x8*>(vb + (size_t)(4 * kg + u) * a.kv_dim + dc * 8);
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = ctid + 256 * i;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int p = kt + 4 * kg + u;
+                f16x8 val = {};
+                if (pr < KCH * (BN / 4) && p >= wg_lo && p <= wg_hi)
+                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + dc * 8);
+                rv[i][u] = val;
+            }
+        }
+    };
+    auto stash_k = [&](int stage) {
+        f16* Ks = K_s + stage * (BN * KPAD);
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = ctid + 256 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            *reinterpret_cast<f16x8*>(&Ks[key * KPAD + col * 8]) = rk[i];
+        }
+    };
+    auto stash_v = [&](int stage) {
+        f16* Vts = Vt_s + stage * (HD * VPAD);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = ctid + 256 * i;
+            if (pr >= KCH * (BN / 4)) continue;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<f16x4*>(&Vts[(dc * 8 + j) * VPAD + 4 * kg]) =
+                    f16x4{rv[i][0][j], rv[i][1][j], rv[i][2][j], rv[i][3][j]};
+        }
+    };
+
+    // ---- the wave's steps
+    // S^T - mb = K Q^T - mb; mb is the running max once one is set.
+    auto qk = [&](const f16* Ks) {
+        mb = m_run > -1e29f ? m_run : 0.f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const f16x8 ka = *reinterpret_cast<const f16x8*>(&Ks[(kb * 32 + l32) * KPAD + 8 * hh + ks * 16]);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[ks], s[kb], 0, 0, 0);
+            }
+    };
+    // s[kb][i] is key kt + 32*kb + 8*(i/4) + 4*hh + i%4 of query qrow.
+    auto mask = [&](int kt) {
+        if (kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min) return;  // wave-uniform
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kt + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                if (key < my_lo || key > my_hi) s[kb][i] = -INFINITY;
+            }
+    };
+    // p = exp2(s) into P (the B operands of the PST k-steps: step st is
+    // registers 8*(st%2) .. +7 of s[st/2]); the lazy-rescale test on the f16
+    // p as in the kernel above; l from the rounded p.
+    constexpr float kSlackP = 256.f;  // 2^kRescaleSlack
+    static_assert(kRescaleSlack == 8.f, "kSlackP is 2^kRescaleSlack");
+    const f16x2 one2 = {(f16)1.f, (f16)1.f};
+    auto softmax = [&]() {
+        auto make_p = [&]() {
+#pragma unroll
+            for (int st = 0; st < PST; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) P[st][j] = (f16)fast_exp2(s[st / 2][8 * (st % 2) + j]);
+        };
+        make_p();
+        f16x2 pm = {P[0][0], P[0][1]};
+#pragma unroll
+        for (int st = 0; st < PST; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{P[st][j], P[st][j + 1]});
+        const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+        if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kb][i]);
+            mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the tile's largest score
+            const float mn = fmaxf(m_run, mt);
+            const float corr = fast_exp2(m_run - mn);
+            m_run = mn;
+            l_run *= corr;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+            // no key seen yet (a masked tile): the scores stay relative to 0
+            const float nmb = mn > -1e29f ? mn : 0.f;
+            const float shift = nmb - mb;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[kb][i] -= shift;
+            mb = nmb;
+            make_p();
+        }
+#pragma unroll
+        for (int st = 0; st < PST; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2)
+                l_run = __builtin_amdgcn_fdot2(f16x2{P[st][j], P[st][j + 1]}, one2, l_run, false);
+    };
+    // O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys 16*st + 4*hh
+    // + {0..3} and 16*st + 8 + 4*hh + {0..3} of the tile.
+    auto pv = [&](const f16* Vts) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 4 * hh];
+#pragma unroll
+            for (int st = 0; st < PST; ++st) {
+                const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
+                const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
+                const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, P[st], o[nb], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- prologue: K(0) staged, K(1) and V(0) in registers
+    if (n_t > 0) {
+        if (grp == 0) {
+            fetch_k(kt_begin);
+            stash_k(0);
+            if (n_t > 1) fetch_k(kt_begin + BN);
+        } else {
+            fetch_v(kt_begin);
+        }
+    }
+    // One loop per group (the group is fixed per wave); both run n_t + 1
+    // iterations of two barriers each.
+    if (grp == 0) {
+        for (int i = 0; i <= n_t; ++i) {
+            const int kt = kt_begin + i * BN;
+            const bool k_in = i >= wi0 && i <= wi1;  // K tile i is the wave's (uniform)
+            const bool v_in = i - 1 >= wi0 && i - 1 <= wi1;
+            __syncthreads();
+            __builtin_amdgcn_s_setprio(1);
+            if (k_in) qk(K_s + (i & 1) * (BN * KPAD));
+            if (v_in) pv(Vt_s + ((i + 1) & 1) * (HD * VPAD));
+            __builtin_amdgcn_s_setprio(0);
+            __syncthreads();
+            if (k_in) {
+                mask(kt);
+                softmax();
+            }
+            if (i + 1 < n_t) stash_k((i + 1) & 1);
+            if (i + 2 < n_t) fetch_k(kt + 2 * BN);
+        }
+    } else {
+        for (int i = 0; i <= n_t; ++i) {
+            const int kt = kt_begin + i * BN;
+            const bool k_in = i >= wi0 && i <= wi1;
+            const bool v_in = i - 1 >= wi0 && i - 1 <= wi1;
+            __syncthreads();
+            if (v_in) {
+                mask(kt - BN);
+                softmax();
+            }
+            if (i < n_t) stash_v(i & 1);
+            if (i + 1 < n_t) fetch_v(kt + BN);
+            __syncthreads();
+            __builtin_amdgcn_s_setprio(1);
+            if (k_in) qk(K_s + (i & 1) * (BN * KPAD));
+            if (v_in) pv(Vt_s + ((i + 1) & 1) * (HD * VPAD));
+            __builtin_amdgcn_s_setprio(0);
+        }
+    }
+
+    // ---- normalize and store: o[nb][i] is dim nb*32 + 8*(i/4) + 4*hh + i%4
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    if (!qvalid) return;
+    const float inv = 1.f / l_tot;
+    float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
+    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride : nullptr;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = nb * 32 + 8 * g4 + 4 * hh;
+            f32x4 y = f32x4{o[nb][4 * g4] * inv, o[nb][4 * g4 + 1] * inv, o[nb][4 * g4 + 2] * inv,
+                            o[nb][4 * g4 + 3] * inv};
+            if (grow) y = gate_sigmoid4(y, grow + d);
+            *reinterpret_cast<f32x4*>(orow + d) = y;
+        }
+}
+
+// The ping-pong kernel takes 256 query rows per workgroup and one workgroup
+// per CU: it pays when there are at least two workgroups per CU (S >= 4096 at
+// 32 heads; at S = 2048 a single round of unequal causal workgroups leaves
+// CUs idle, and the 128-row kernel is faster).  LMX_PREFILL_KERNEL=pp|tile
+// forces one of them (read on every call, for tests and sweeps).
+static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
+    if (hd != 128) return false;
+    if (const char* e = std::getenv("LMX_PREFILL_KERNEL")) {
+        if (!std::strcmp(e, "pp")) return true;
+        if (!std::strcmp(e, "tile")) return false;
+    }
+    return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
+}
+
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
     (void)q_dt;
     return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
@@ -402,14 +793,21 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     a.n_tokens = (int)p->n_tokens;
     a.bidi = (int)p->bidi;
     a.c = p->scale * kLog2e;
-    a.n_qtiles = (a.n_tokens + kPfBM - 1) / kPfBM;
+    const int hd = (int)p->head_dim;
+    const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
+    const int bm = pp ? kPpBM : kPfBM;
+    a.n_qtiles = (a.n_tokens + bm - 1) / bm;
     const long nblk = (long)a.n_qtiles * a.H;
     if (nblk > INT_MAX) return LMX_E_SHAPE;
     dim3 grid((unsigned)nblk);
     (void)hipGetLastError();
-    const int hd = (int)p->head_dim;
 #define LMX_PF(QT, HDV) hipLaunchKernelGGL((attn_prefill_kernel<QT, HDV>), grid, dim3(256), 0, st, a)
-    if (q_dt == LMX_F16) {
+    if (pp) {
+        if (q_dt == LMX_F16)
+            hipLaunchKernelGGL((attn_prefill_pp_kernel<f16, 128>), grid, dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_prefill_pp_kernel<float, 128>), grid, dim3(512), 0, st, a);
+    } else if (q_dt == LMX_F16) {
         if (hd == 64) LMX_PF(f16, 64);
         else if (hd == 128) LMX_PF(f16, 128);
         else if (hd == 256) LMX_PF(f16, 256);

@@ -91,3 +91,10 @@ def test_prefill_f16_queries_with_separate_gate():
 @pytest.mark.parametrize("t", [1, 96])
 def test_strided_queries_without_gate(t):
     run(7, t=t, H=8, Hkv=2, hd=128, n_pos=300, base=300 - t, gated=False)
+
+
+@pytest.mark.parametrize("q_f16", [False, True])
+def test_prefill_ping_pong_kernel_gated(q_f16, monkeypatch):
+    # the head_dim-128 ping-pong prefill kernel, forced at a small size
+    monkeypatch.setenv("LMX_PREFILL_KERNEL", "pp")
+    run(8, t=300, H=8, Hkv=2, hd=128, n_pos=340, base=40, q_f16=q_f16)

@@ -19,11 +19,25 @@ pytestmark = pytest.mark.gpu
 import llmoxide_amd as lmx  # noqa: E402
 
 
+@pytest.fixture(autouse=True, params=["tile", "pp"])
+def prefill_kernel(request, monkeypatch):
+    """Every case on both prefill kernels: the 128-row tile kernel and the
+    ping-pong kernel (head_dim 128 only; other head sizes use the tile kernel
+    under either setting)."""
+    monkeypatch.setenv("LMX_PREFILL_KERNEL", request.param)
+    return request.param
+
+
 def dev(a, dtype=None):
     t = torch.from_numpy(np.ascontiguousarray(a))
     if dtype is not None:
         t = t.view(dtype)
     return t.cuda()
+
+
+def lmx_kernel():
+    import os
+    return os.environ.get("LMX_PREFILL_KERNEL", "auto")
 
 
 def say(*a):
@@ -52,7 +66,7 @@ def gpu_attn(c: AttnCase, *, base, window=0, bidi=False, scale=None, ring=False,
 
 
 def check(c, *, base, window=0, bidi=False, scale=None, ring=False, k_cur=False):
-    say(f"prefill t={c.t} H={c.H} Hkv={c.Hkv} hd={c.hd} base={base} w={window} bidi={bidi} "
+    say(f"prefill[{lmx_kernel()}] t={c.t} H={c.H} Hkv={c.Hkv} hd={c.hd} base={base} w={window} bidi={bidi} "
         f"ring={ring} k_cur={k_cur} q_f16={c.q_f16}")
     got = gpu_attn(c, base=base, window=window, bidi=bidi, scale=scale, ring=ring, k_cur=k_cur)
     ref = c.reference(base_pos=base, window=window, bidi=bidi, scale=scale)
