@@ -350,15 +350,26 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 
             // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
             //      32*kb + 16*st + 4*hh + {0..3} and + 8 + 4*hh + {0..3}.
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
+            //      Block nb+1's operands are read while block nb's MFMAs run.
+            auto load = [&](int nb, f16x8 (&va)[2]) {
                 const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 32 * kb + 4 * hh];
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
                     const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
                     const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
-                    const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf[st], o[nb], 0, 0, 0);
+                    va[st] = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                }
+            };
+            f16x8 va[2][2];
+            load(0, va[0]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if (nb + 1 < NB) load(nb + 1, va[(nb + 1) & 1]);
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[nb & 1][st], pf[st], o[nb], 0, 0, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then two LDS reads
                 }
             }
         }
@@ -670,16 +681,29 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     };
     // O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys 16*st + 4*hh
     // + {0..3} and 16*st + 8 + 4*hh + {0..3} of the tile.
+    // The A operands of output block nb+1 are read from LDS while block nb's
+    // MFMAs run (one read in flight per MFMA would wait out the LDS latency
+    // every time).
     auto pv = [&](const f16* Vts) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
+        auto load = [&](int nb, f16x8 (&va)[PST]) {
             const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 4 * hh];
 #pragma unroll
             for (int st = 0; st < PST; ++st) {
                 const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
                 const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
-                const f16x8 va = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, P[st], o[nb], 0, 0, 0);
+                va[st] = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            }
+        };
+        f16x8 va[2][PST];
+        load(0, va[0]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            if (nb + 1 < NB) load(nb + 1, va[(nb + 1) & 1]);
+#pragma unroll
+            for (int st = 0; st < PST; ++st) {
+                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[nb & 1][st], P[st], o[nb], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then two LDS reads
             }
         }
     };
