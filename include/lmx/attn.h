@@ -173,7 +173,9 @@ lmx_status lmx_attn_prologue(const lmx_prologue_desc *d, float *q, const float *
  * case (LMX_E_RING_HAZARD) unless k_cur/v_cur are given.
  * q_dt: LMX_F32 or LMX_F16.  kv_dt: LMX_F16.
  * Workspace: lmx_attn_workspace_bytes(p) bytes, zeroed once by
- * lmx_workspace_init; 0 bytes may be asked for (ws may then be NULL).
+ * lmx_workspace_init; 0 bytes may be asked for (ws may then be NULL).  It
+ * holds the split partials of decode, and of prefill when a short batch on a
+ * long cache is cut into key splits to fill the GPU.
  */
 size_t lmx_attn_workspace_bytes(const lmx_attn_params *p);
 

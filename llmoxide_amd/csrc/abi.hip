@@ -21,9 +21,10 @@ lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, cons
                           lmx_dtype q_dt, float* out, void* ws, size_t ws_bytes, hipStream_t st);
 // attn_prefill.hip
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt);
+size_t prefill_workspace_bytes(const lmx_attn_params* p);
 lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
                        const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
-                       float* out, hipStream_t st);
+                       float* out, void* ws, size_t ws_bytes, hipStream_t st);
 // qmatvec.hip
 lmx_status qmatvec(const lmx_qmv_desc* d, const void* w, const float* x, float* y, hipStream_t st);
 // deltanet.hip
@@ -236,10 +237,14 @@ lmx_status lmx_attn_prologue(const lmx_prologue_desc* d, float* q, const float* 
 
 size_t lmx_attn_workspace_bytes(const lmx_attn_params* p) {
     if (check_attn_params(p) != LMX_OK) return 0;
-    // The split-K path is the only one with a workspace; f32 q is the case
-    // that decides between the paths most conservatively.
-    if (!use_split_k(p, LMX_F32) && !use_split_k(p, LMX_F16)) return 0;
-    return decode_workspace_bytes(p);
+    // The split-K decode path and a key-split prefill use a workspace; the
+    // size covers whichever path either query dtype takes.
+    size_t need = 0;
+    for (lmx_dtype dt : {LMX_F32, LMX_F16}) {
+        const size_t b = use_split_k(p, dt) ? decode_workspace_bytes(p) : prefill_workspace_bytes(p);
+        if (b > need) need = b;
+    }
+    return need;
 }
 
 lmx_status lmx_attn_fwd(const lmx_attn_params* p, const void* q, lmx_dtype q_dt,
@@ -288,7 +293,8 @@ lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, con
     if (use_split_k(p, q_dt))
         return decode_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
                           (hipStream_t)stream);
-    return prefill_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, (hipStream_t)stream);
+    return prefill_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
+                       (hipStream_t)stream);
 }
 
 size_t lmx_attn_decode_batched_workspace_bytes(const lmx_attn_params* p, int32_t n_seq,

@@ -41,6 +41,12 @@ struct PrefillArgs {
     int base_pos, window, n_tokens, bidi;
     int n_qtiles;
     float c;  // scale * log2(e)
+    // Key-range split (attn_prefill_kernel only): n_split > 1 writes each
+    // split's unnormalized o and its (m, l) to part_o / part_ml for
+    // prefill_merge_kernel.
+    int n_split;
+    float* part_o;   // [n_split][t][H][hd]
+    float* part_ml;  // [n_split][t][H][2]
 };
 
 constexpr int kPfBM = 128;  // query rows per workgroup
@@ -77,14 +83,17 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
     __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
 
-    // ---- which (head, query tile) this workgroup owns
+    // ---- which (head, query tile, key split) this workgroup owns
     const int nblk = gridDim.x;
     const int logical = xcd_remap(blockIdx.x, nblk);
-    const int per_kvh = a.n_qtiles * a.G;
+    const int n_split = a.n_split;
+    const int per_kvh = a.n_qtiles * a.G * n_split;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
-    const int qt = a.n_qtiles - 1 - rem / a.G;
-    const int h = kvh * a.G + (rem % a.G);
+    const int qt = a.n_qtiles - 1 - rem / (a.G * n_split);
+    const int rem2 = rem % (a.G * n_split);
+    const int h = kvh * a.G + rem2 / n_split;
+    const int sp = rem2 % n_split;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hh = lane >> 5;
@@ -242,15 +251,20 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         }
     };
 
-    const int kt_begin = (wg_lo / BN) * BN;
-    if (kt_begin <= wg_hi) fetch(kt_begin);
+    // This workgroup's split: chunk sp of the tiles covering [wg_lo, wg_hi].
+    const int kt_all = (wg_lo / BN) * BN;
+    const int n_t_all = wg_lo <= wg_hi ? (wg_hi - kt_all) / BN + 1 : 0;
+    const int cs = (n_t_all + n_split - 1) / n_split;
+    const int kt_begin = kt_all + sp * cs * BN;
+    const int kt_stop = min(wg_hi, kt_begin + cs * BN - 1);
+    if (kt_begin <= kt_stop) fetch(kt_begin);
     int stage = 0;
-    for (int kt = kt_begin; kt <= wg_hi; kt += BN, stage ^= 1) {
+    for (int kt = kt_begin; kt <= kt_stop; kt += BN, stage ^= 1) {
         // Stage `stage` was last read two tiles ago, before the barrier of
         // the previous iteration: writing it now needs no extra barrier.
         stash(stage);
         __syncthreads();
-        if (kt + BN <= wg_hi) fetch(kt + BN);
+        if (kt + BN <= kt_stop) fetch(kt + BN);
         if (!wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
         const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
         const f16* Ks = K_s + stage * (BN * KPAD);
@@ -378,6 +392,20 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     // ---- normalize and store: o[nb][i] is dim nb*32 + 8*(i/4) + 4*hh + i%4
     const float l_tot = l_run + shfl_xor(l_run, 32);
     if (!qvalid) return;
+    if (n_split > 1) {
+        // the split's partial: o as accumulated, and (m, l); an empty split
+        // leaves m = -1e30, l = 0, o = 0
+        const size_t row = ((size_t)sp * t + qrow) * a.H + h;
+        if (hh == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * row) = f32x2{m_run, l_tot};
+        float* prow = a.part_o + row * HD;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+                *reinterpret_cast<f32x4*>(prow + nb * 32 + 8 * g4 + 4 * hh) =
+                    f32x4{o[nb][4 * g4], o[nb][4 * g4 + 1], o[nb][4 * g4 + 2], o[nb][4 * g4 + 3]};
+        return;
+    }
     const float inv = 1.f / l_tot;
     float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
     const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride : nullptr;
@@ -391,6 +419,35 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             if (grow) y = gate_sigmoid4(y, grow + d);
             *reinterpret_cast<f32x4*>(orow + d) = y;
         }
+}
+
+// Combines the n_split partials of each (query row, head): with M the largest
+// split max, out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, splits in
+// order, then the output gate.  One thread per 4 output dims.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int hd) {
+    const int n_rows = a.n_tokens * a.H;
+    const int c4n = hd / 4;
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long)n_rows * c4n) return;
+    const int row = (int)(idx / c4n), c4 = (int)(idx % c4n);
+    float M = -INFINITY;
+    for (int sp = 0; sp < a.n_split; ++sp) M = fmaxf(M, a.part_ml[2 * ((size_t)sp * n_rows + row)]);
+    float L = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < a.n_split; ++sp) {
+        const size_t r = (size_t)sp * n_rows + row;
+        const f32x2 ml = *reinterpret_cast<const f32x2*>(a.part_ml + 2 * r);
+        const float wgt = fast_exp2(ml[0] - M);
+        L += wgt * ml[1];
+        const f32x4 ov = *reinterpret_cast<const f32x4*>(a.part_o + r * hd + 4 * c4);
+        acc += wgt * ov;
+    }
+    f32x4 y = acc * (1.f / L);
+    if (a.gate) {
+        const int qrow = row / a.H, h = row % a.H;
+        y = gate_sigmoid4(y, a.gate + ((size_t)qrow * a.H + h) * a.gate_stride + 4 * c4);
+    }
+    *reinterpret_cast<f32x4*>(a.out + (size_t)row * hd + 4 * c4) = y;
 }
 
 // ---- Ping-pong variant (head_dim <= 128) -----------------------------------
@@ -790,6 +847,40 @@ static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
     return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
 }
 
+// Key splits for attn_prefill_kernel.  When the query tiles give fewer
+// workgroups than the CUs hold at once (two per CU, one at head_dim 256), as
+// for a short chunk on a long cache, each tile's key range is cut into splits
+// until that many are in flight, keeping at least kMinSplitTiles tiles per
+// split; a merge kernel combines them.
+constexpr int kMinSplitTiles = 8;
+constexpr int kMaxSplits = 16;
+constexpr int kCus = 256;
+int decode_max_vis(const lmx_attn_params* p);
+static int prefill_splits(const lmx_attn_params* p) {
+    const int hd = (int)p->head_dim;
+    if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads)) return 1;
+    const long n_wg = (long)((p->n_tokens + kPfBM - 1) / kPfBM) * p->n_heads;
+    const long slots = (long)kCus * (hd > 128 ? 1 : 2);
+    if (n_wg >= slots) return 1;
+    const int bn = hd >= 256 ? 32 : 64;
+    // the longest key range a workgroup covers: one query's range plus the
+    // spread of the tile's positions
+    const long tiles = ((long)decode_max_vis(p) + kPfBM + bn - 1) / bn + 1;
+    long sp = (slots + n_wg - 1) / n_wg;
+    if (sp > tiles / kMinSplitTiles) sp = tiles / kMinSplitTiles;
+    if (sp > kMaxSplits) sp = kMaxSplits;
+    return sp < 2 ? 1 : (int)sp;
+}
+
+static size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
+
+size_t prefill_workspace_bytes(const lmx_attn_params* p) {
+    const int sp = prefill_splits(p);
+    if (sp == 1) return 0;
+    const size_t rows = (size_t)sp * p->n_tokens * p->n_heads;
+    return round_up256(rows * 2 * sizeof(float)) + round_up256(rows * p->head_dim * sizeof(float));
+}
+
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
     (void)q_dt;
     return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
@@ -797,8 +888,16 @@ bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
 
 lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
                        const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
-                       float* out, hipStream_t st) {
+                       float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     PrefillArgs a{};
+    a.n_split = prefill_splits(p);
+    if (a.n_split > 1) {
+        if (!ws || ws_bytes < prefill_workspace_bytes(p)) return LMX_E_WORKSPACE;
+        if (((uintptr_t)ws & 255) != 0) return LMX_E_ALIGN;
+        const size_t rows = (size_t)a.n_split * p->n_tokens * p->n_heads;
+        a.part_ml = static_cast<float*>(ws);
+        a.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + round_up256(rows * 2 * sizeof(float)));
+    }
     a.q = q;
     a.q_stride = io.q_stride;
     a.gate = io.gate;
@@ -821,7 +920,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
     const int bm = pp ? kPpBM : kPfBM;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
-    const long nblk = (long)a.n_qtiles * a.H;
+    const long nblk = (long)a.n_qtiles * a.H * a.n_split;
     if (nblk > INT_MAX) return LMX_E_SHAPE;
     dim3 grid((unsigned)nblk);
     (void)hipGetLastError();
@@ -843,6 +942,10 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
         else return LMX_E_UNSUPPORTED;
     }
 #undef LMX_PF
+    if (a.n_split > 1) {
+        const long items = (long)a.n_tokens * a.H * (hd / 4);
+        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, a, hd);
+    }
     LMX_CHECK_LAUNCH();
     return LMX_OK;
 }

@@ -98,3 +98,10 @@ def test_prefill_ping_pong_kernel_gated(q_f16, monkeypatch):
     # the head_dim-128 ping-pong prefill kernel, forced at a small size
     monkeypatch.setenv("LMX_PREFILL_KERNEL", "pp")
     run(8, t=300, H=8, Hkv=2, hd=128, n_pos=340, base=40, q_f16=q_f16)
+
+
+@pytest.mark.parametrize("q_f16", [False, True])
+def test_prefill_key_split_merge_gated(q_f16):
+    # a short chunk on a long cache: the keys are cut into splits whose
+    # partials the merge kernel combines and gates
+    run(9, t=100, H=8, Hkv=2, hd=128, n_pos=3100, base=3000, q_f16=q_f16)

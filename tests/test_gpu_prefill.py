@@ -126,8 +126,9 @@ def test_gemma_global_prefill():
 
 
 @pytest.mark.parametrize("window", [0, 64, 200])
-def test_bidirectional_prefill(window):
-    c = AttnCase(900 + window, t=300, H=8, Hkv=4, hd=64, n_pos=400, q_f16=True)
+@pytest.mark.parametrize("hd", [64, 128])
+def test_bidirectional_prefill(window, hd):
+    c = AttnCase(900 + window + hd, t=300, H=8, Hkv=4, hd=hd, n_pos=400, q_f16=True)
     check(c, base=100, window=window, bidi=True, ring=bool(window), k_cur=bool(window))
 
 
