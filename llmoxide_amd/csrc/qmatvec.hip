@@ -11,7 +11,8 @@
 // reference repacks Q6_K to 224 bytes at upload, this kernel instead loads
 // the dwords that cover a 2-byte aligned field and funnel-shifts them).
 //
-// Work split.  A workgroup of four waves stages x [n_tok, in_dim] in LDS once,
+// Work split (the direct kernel; the staged one is described at
+// qmatvec_lds_kernel).  A workgroup of four waves stages x [n_tok, in_dim] in LDS once,
 // then its waves take row groups of RW = 4 rows in turn (the grid is capped,
 // so a workgroup serves many groups).  Lane l takes 64-weight units l,
 // l + 64, ... of the rows (a Q6_K unit is a quarter of a half-block), reads
@@ -49,12 +50,17 @@ template <> struct QTraits<kF32> { static constexpr int unit = 64, bbytes = 4, b
 template <> struct QTraits<kF16> { static constexpr int unit = 64, bbytes = 2, belems = 1; };
 template <> struct QTraits<kBF16> { static constexpr int unit = 64, bbytes = 2, belems = 1; };
 
-// Weight bytes are streamed: read once, never reused.
+// Weight bytes are streamed: read once, never reused.  LDS: the bytes were
+// staged in a wave's LDS slice first (qmatvec_lds_kernel).
+template <bool LDS>
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    if constexpr (LDS) return *reinterpret_cast<const uint32_t*>(p);
+    else return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
+template <bool LDS>
 __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+    if constexpr (LDS) return *reinterpret_cast<const uint16_t*>(p);
+    else return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
 // N dwords of the byte range [p, p + 4N) at a 2-byte aligned p: the aligned
@@ -62,16 +68,18 @@ __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
 // reads exactly its own bytes; a shifted one also reads the 2 bytes before
 // and after it, which for every field below lie inside the same block or the
 // block before (a shifted block is never the first of the matrix).
-template <int N>
+template <int N, bool LDS>
 __device__ __forceinline__ void ld_words_a2(const uint8_t* p, uint32_t (&out)[N]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);  // 0 or 2
+    // base by pointer arithmetic, not an integer round trip, so the loads
+    // stay global ones (a flat load also counts against the LDS wait counter,
+    // and every read of the staged x would wait for the weight stream)
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);  // 0 or 2
+    const uint8_t* base = p - sh;
     uint32_t raw[N + 1];
 #pragma unroll
-    for (int i = 0; i < N; ++i) raw[i] = ld_u32(base + 4 * i);
+    for (int i = 0; i < N; ++i) raw[i] = ld_u32<LDS>(base + 4 * i);
     raw[N] = 0u;
-    if (sh) raw[N] = ld_u32(base + 4 * N);
+    if (sh) raw[N] = ld_u32<LDS>(base + 4 * N);
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
@@ -96,17 +104,19 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&s)[3], int j, flo
 
 // The dot products of one unit of the RW rows with the T staged tokens,
 // added into acc[r][t].  `row[r]` points at row r's bytes (for a row past the
-// end, the wave's first row again: its result is never stored).
-template <int TY, int T>
-__device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], int u, const float* xs,
-                                         int in_dim, float (&acc)[kQmvRows][T]) {
+// end, the wave's first row again: its result is never stored); uw is the
+// unit's index from row[r], ux its index in x (they differ when row[r] is a
+// staged chunk of the row).
+template <int TY, int T, bool LDS>
+__device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], int uw, int ux,
+                                         const float* xs, int in_dim, float (&acc)[kQmvRows][T]) {
     if constexpr (TY == kQ4K) {
         // unit u = pair p of block b: sub-blocks 2p (low nibbles of 32 bytes)
         // and 2p + 1 (high nibbles); x chunk [256b + 64p, +64).  The x chunk
         // is walked in steps of four elements (per token), each step applied
         // to all rows, so only a step of x is live at a time.
-        const int b = u >> 2, p = u & 3;
-        const float* xc = xs + 256 * b + 64 * p;
+        const int b = uw >> 2, p = uw & 3;
+        const float* xc = xs + 64 * ux;
         uint32_t q[kQmvRows][8];
         float a1[kQmvRows], c1[kQmvRows], a2[kQmvRows], c2[kQmvRows];
 #pragma unroll
@@ -114,9 +124,9 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             const uint8_t* blk = row[r] + (size_t)b * 144;
             uint32_t hdr[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) hdr[i] = ld_u32(blk + 4 * i);
+            for (int i = 0; i < 4; ++i) hdr[i] = ld_u32<LDS>(blk + 4 * i);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) q[r][i] = ld_u32(blk + 16 + 32 * p + 4 * i);
+            for (int i = 0; i < 8; ++i) q[r][i] = ld_u32<LDS>(blk + 16 + 32 * p + 4 * i);
             const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
             const uint32_t sc3[3] = {hdr[1], hdr[2], hdr[3]};
             float sc1, m1, sc2, m2;
@@ -163,19 +173,19 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         // elements 32g + l of the half with l in [16k, 16k + 16), g < 4.
         // Element 32g + l takes the quant of quant.rs:99-106 from ql[l] (g 0,
         // 2) or ql[l + 32] (g 1, 3) and qh[l], and scale 2g + k (l / 16 = k).
-        const int b = u >> 2, h = (u >> 1) & 1, k = u & 1;
-        const float* xc = xs + 256 * b + 128 * h + 16 * k;
+        const int b = uw >> 2, h = (uw >> 1) & 1, k = uw & 1;
+        const float* xc = xs + 64 * (ux & ~3) + 128 * h + 16 * k;
         uint32_t qa[kQmvRows][4], qb[kQmvRows][4], qh[kQmvRows][4];
         float sc[kQmvRows][4], dd[kQmvRows];
 #pragma unroll
         for (int r = 0; r < kQmvRows; ++r) {
             const uint8_t* blk = row[r] + (size_t)b * 210;
             uint32_t scw[2];
-            ld_words_a2<4>(blk + 64 * h + 16 * k, qa[r]);
-            ld_words_a2<4>(blk + 64 * h + 32 + 16 * k, qb[r]);
-            ld_words_a2<4>(blk + 128 + 32 * h + 16 * k, qh[r]);
-            ld_words_a2<2>(blk + 192 + 8 * h, scw);  // this half's 8 i8 scales
-            dd[r] = (float)__builtin_bit_cast(f16, ld_u16(blk + 208));
+            ld_words_a2<4, LDS>(blk + 64 * h + 16 * k, qa[r]);
+            ld_words_a2<4, LDS>(blk + 64 * h + 32 + 16 * k, qb[r]);
+            ld_words_a2<4, LDS>(blk + 128 + 32 * h + 16 * k, qh[r]);
+            ld_words_a2<2, LDS>(blk + 192 + 8 * h, scw);  // this half's 8 i8 scales
+            dd[r] = (float)__builtin_bit_cast(f16, ld_u16<LDS>(blk + 208));
 #pragma unroll
             for (int g = 0; g < 4; ++g) sc[r][g] = sbyte_f(scw[(2 * g + k) >> 2], (2 * g + k) & 3);
         }
@@ -229,7 +239,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             }
     } else if constexpr (TY == kQ8_0) {
         // unit u = blocks 2u, 2u + 1: 68 bytes at 68u (4-byte aligned)
-        const float* xc = xs + 64 * u;
+        const float* xc = xs + 64 * ux;
         float X0[T], X1[T];  // the x sums of the two blocks, shared by all rows
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -246,10 +256,10 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         }
 #pragma unroll
         for (int r = 0; r < kQmvRows; ++r) {
-            const uint8_t* p = row[r] + (size_t)68 * u;
+            const uint8_t* p = row[r] + (size_t)68 * uw;
             uint32_t wds[17];
 #pragma unroll
-            for (int i = 0; i < 17; ++i) wds[i] = ld_u32(p + 4 * i);
+            for (int i = 0; i < 17; ++i) wds[i] = ld_u32<LDS>(p + 4 * i);
             const float d0 = f16_lo(wds[0]), d1 = f16_hi(wds[8]);
             // block 0 quants: bytes 2..33 -> words 0..8 shifted by 2;
             // block 1 quants: bytes 36..67 -> words 9..16
@@ -279,7 +289,8 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         }
     } else {
         // dense rows: 64 consecutive weights
-        const float* xc = xs + 64 * u;
+        const int u = uw;
+        const float* xc = xs + 64 * ux;
 #pragma unroll
         for (int r = 0; r < kQmvRows; ++r) {
             float wv[64];
@@ -352,7 +363,7 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_kernel(QmvArgs a) {
         for (int r = 0; r < kQmvRows; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
-        for (int u = lane; u < n_units; u += 64) unit_dot<TY, T>(row, u, xs, a.in_dim, acc);
+        for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false>(row, u, u, xs, a.in_dim, acc);
 #pragma unroll
         for (int r = 0; r < kQmvRows; ++r) {
 #pragma unroll
@@ -362,6 +373,121 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_kernel(QmvArgs a) {
             }
         }
     }
+}
+
+// ---- Staged variant for the block formats ----------------------------------
+//
+// The per-unit reads above give each lane 2-16 bytes at a stride of a block:
+// one load instruction touches 30-50 cache lines and every line is touched
+// again by the next field's load, which keeps the texture addresser busy and
+// holds the stream well below HBM rate.  Here a wave copies a chunk of 64
+// units of each of its RW rows (16 K-quant blocks, or 128 Q8_0 blocks) into
+// its own LDS slice with contiguous 16-byte LDS-DMA loads (the 16-aligned
+// window around the chunk, 1 KB per instruction), then runs the same unit_dot
+// from LDS.  The slice is private to the wave, so a wait for its own loads
+// (vmcnt) is the only synchronisation.  The row group holding the matrix's
+// last row takes the direct path, so no window reaches past the matrix.
+// Q6_K and Q8_0 take this kernel (lm_head 151936 x 4096 Q6_K: 2.36 -> 4.0
+// TB/s).  Q4_K stays direct: a lane's 32 quant bytes already lie next to its
+// neighbours', and staging measured slower there.
+template <int TY>
+struct QChunk;
+// units per byte group, bytes per group, DMA instructions per row and chunk
+template <> struct QChunk<kQ4K> { static constexpr int upg = 4, gbytes = 144, ni = 3; };
+template <> struct QChunk<kQ6K> { static constexpr int upg = 4, gbytes = 210, ni = 4; };
+template <> struct QChunk<kQ8_0> { static constexpr int upg = 1, gbytes = 68, ni = 5; };
+template <int TY>
+constexpr size_t qmv_slice_bytes() { return (size_t)kQmvRows * QChunk<TY>::ni * 1024; }
+
+template <int TY, int T>
+__global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    constexpr int NI = QChunk<TY>::ni, UPG = QChunk<TY>::upg, GB = QChunk<TY>::gbytes;
+    constexpr int CB = 64 / UPG * GB;  // bytes of a full 64-unit chunk of a row
+    static_assert((64 / UPG * GB + 15) / 16 + 1 <= NI * 64, "DMA instructions cover a chunk's window");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nx4 = a.n_tok * a.in_dim / 4;
+    for (int i = tid; i < nx4; i += kQmvWaves * 64)
+        reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(a.x)[i];
+    __syncthreads();
+    uint8_t* slice = reinterpret_cast<uint8_t*>(xs + a.n_tok * a.in_dim) + wave * qmv_slice_bytes<TY>();
+
+    const int n_groups = (a.rows + kQmvRows - 1) / kQmvRows;
+    const int n_units = a.in_dim / QTraits<TY>::unit;
+    const int n_chunks = (n_units + 63) / 64;
+    for (int g = blockIdx.x * kQmvWaves + wave; g < n_groups; g += gridDim.x * kQmvWaves) {
+        const int r0 = g * kQmvRows;
+        float acc[kQmvRows][T];
+#pragma unroll
+        for (int r = 0; r < kQmvRows; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
+        if (r0 + kQmvRows >= a.rows) {
+            // the group with the matrix's last row: direct reads, exact bytes
+            const uint8_t* row[kQmvRows];
+#pragma unroll
+            for (int r = 0; r < kQmvRows; ++r) {
+                const int rr = r0 + r < a.rows ? r0 + r : r0;
+                row[r] = a.w + (size_t)rr * a.row_bytes;
+            }
+            for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false>(row, u, u, xs, a.in_dim, acc);
+        } else {
+            for (int c = 0; c < n_chunks; ++c) {
+                const int cu = min(64, n_units - 64 * c);  // units in this chunk
+                const size_t len = (size_t)(cu / UPG) * GB;
+                const uint8_t* lrow[kQmvRows];
+#pragma unroll
+                for (int r = 0; r < kQmvRows; ++r) {
+                    const size_t s0 = (size_t)(r0 + r) * a.row_bytes + (size_t)c * CB;
+                    const size_t w0 = s0 & ~(size_t)15;
+                    const int n16 = (int)((s0 + len - w0 + 15) / 16);
+                    uint8_t* dst = slice + r * (NI * 1024);
+#pragma unroll
+                    for (int j = 0; j < NI; ++j) {
+                        const int i = min(64 * j + lane, n16 - 1);  // every lane loads: a fixed count
+                        __builtin_amdgcn_global_load_lds(
+                            (const __attribute__((address_space(1))) void*)(a.w + w0 + 16 * (size_t)i),
+                            (__attribute__((address_space(3))) void*)(dst + 1024 * j), 16, 0, 0);
+                    }
+                    lrow[r] = dst + (s0 - w0);
+                }
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slice holds the chunk
+                if (lane < cu) unit_dot<TY, T, true>(lrow, lane, 64 * c + lane, xs, a.in_dim, acc);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kQmvRows; ++r) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float sum = wave_sum64(acc[r][t]);
+                if (lane == 0 && r0 + r < a.rows) a.y[(size_t)t * a.rows + r0 + r] = sum;
+            }
+        }
+    }
+}
+
+template <int TY>
+static lmx_status launch_lds(const QmvArgs& a, int T, hipStream_t st) {
+    const long groups = (a.rows + kQmvRows - 1) / kQmvRows;
+    const long wgs = std::min<long>((groups + kQmvWaves - 1) / kQmvWaves, kQmvMaxWgs);
+    const dim3 grid((unsigned)wgs);
+    const size_t lds = (size_t)T * a.in_dim * sizeof(float) + kQmvWaves * qmv_slice_bytes<TY>();
+    switch (T) {
+#define LMX_QMV(TT)                                                                                 \
+    case TT: {                                                                                      \
+        static const bool attr = hipFuncSetAttribute((const void*)qmatvec_lds_kernel<TY, TT>,       \
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                                                     160 * 1024) == hipSuccess;                      \
+        if (!attr) return LMX_E_LAUNCH;                                                             \
+        hipLaunchKernelGGL((qmatvec_lds_kernel<TY, TT>), grid, dim3(kQmvWaves * 64), lds, st, a);    \
+        break;                                                                                      \
+    }
+        LMX_QMV(1) LMX_QMV(2) LMX_QMV(3) LMX_QMV(4)
+#undef LMX_QMV
+        default: return LMX_E_UNSUPPORTED;
+    }
+    return LMX_OK;
 }
 
 template <int TY>
@@ -411,9 +537,9 @@ lmx_status qmatvec(const lmx_qmv_desc* d, const void* w, const float* x, float* 
         a.row_bytes = row_bytes;
         lmx_status s;
         switch (d->type) {
-            case kQ4K: s = launch_type<kQ4K>(a, T, st); break;
-            case kQ6K: s = launch_type<kQ6K>(a, T, st); break;
-            case kQ8_0: s = launch_type<kQ8_0>(a, T, st); break;
+            case kQ4K: s = launch_type<kQ4K>(a, T, st); break;  // its loads are contiguous already
+            case kQ6K: s = launch_lds<kQ6K>(a, T, st); break;
+            case kQ8_0: s = launch_lds<kQ8_0>(a, T, st); break;
             case kF32: s = launch_type<kF32>(a, T, st); break;
             case kF16: s = launch_type<kF16>(a, T, st); break;
             default: s = launch_type<kBF16>(a, T, st); break;
