@@ -26,7 +26,8 @@ namespace lmx {
 
 enum QType { kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4K = 12, kQ6K = 14, kBF16 = 30 };
 
-constexpr int kQmvRows = 4;     // rows per wave
+constexpr int kQmvRows = 4;     // rows per wave (direct kernel)
+constexpr int kQmvLdsRows = 2;  // rows per wave (staged kernel: fewer registers, more waves)
 constexpr int kQmvWaves = 4;    // waves per workgroup
 constexpr int kQmvMaxTok = 4;   // tokens per launch
 constexpr int kQmvLdsFloats = 16384;  // x staged in LDS: n_tok * in_dim <= this
@@ -107,9 +108,9 @@ __device__ __forceinline__ void q4k_scale_min(const uint32_t (&s)[3], int j, flo
 // end, the wave's first row again: its result is never stored); uw is the
 // unit's index from row[r], ux its index in x (they differ when row[r] is a
 // staged chunk of the row).
-template <int TY, int T, bool LDS>
-__device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], int uw, int ux,
-                                         const float* xs, int in_dim, float (&acc)[kQmvRows][T]) {
+template <int TY, int T, bool LDS, int RW>
+__device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[RW], int uw, int ux,
+                                         const float* xs, int in_dim, float (&acc)[RW][T]) {
     if constexpr (TY == kQ4K) {
         // unit u = pair p of block b: sub-blocks 2p (low nibbles of 32 bytes)
         // and 2p + 1 (high nibbles); x chunk [256b + 64p, +64).  The x chunk
@@ -117,10 +118,10 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         // to all rows, so only a step of x is live at a time.
         const int b = uw >> 2, p = uw & 3;
         const float* xc = xs + 64 * ux;
-        uint32_t q[kQmvRows][8];
-        float a1[kQmvRows], c1[kQmvRows], a2[kQmvRows], c2[kQmvRows];
+        uint32_t q[RW][8];
+        float a1[RW], c1[RW], a2[RW], c2[RW];
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r) {
+        for (int r = 0; r < RW; ++r) {
             const uint8_t* blk = row[r] + (size_t)b * 144;
             uint32_t hdr[4];
 #pragma unroll
@@ -137,12 +138,12 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             a2[r] = d * sc2;
             c2[r] = dmin * m2;
         }
-        float S1[kQmvRows][T], S2[kQmvRows][T], X1[T], X2[T];
+        float S1[RW][T], S2[RW][T], X1[T], X2[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             X1[t] = X2[t] = 0.f;
 #pragma unroll
-            for (int r = 0; r < kQmvRows; ++r) S1[r][t] = S2[r][t] = 0.f;
+            for (int r = 0; r < RW; ++r) S1[r][t] = S2[r][t] = 0.f;
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -153,7 +154,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
                 X1[t] += (xa[0] + xa[1]) + (xa[2] + xa[3]);
                 X2[t] += (xb[0] + xb[1]) + (xb[2] + xb[3]);
 #pragma unroll
-                for (int r = 0; r < kQmvRows; ++r) {
+                for (int r = 0; r < RW; ++r) {
                     const uint32_t lo = q[r][i] & 0x0F0F0F0Fu, hi = (q[r][i] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -164,7 +165,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             }
         }
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r)
+        for (int r = 0; r < RW; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t)
                 acc[r][t] += a1[r] * S1[r][t] - c1[r] * X1[t] + a2[r] * S2[r][t] - c2[r] * X2[t];
@@ -175,10 +176,10 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         // 2) or ql[l + 32] (g 1, 3) and qh[l], and scale 2g + k (l / 16 = k).
         const int b = uw >> 2, h = (uw >> 1) & 1, k = uw & 1;
         const float* xc = xs + 64 * (ux & ~3) + 128 * h + 16 * k;
-        uint32_t qa[kQmvRows][4], qb[kQmvRows][4], qh[kQmvRows][4];
-        float sc[kQmvRows][4], dd[kQmvRows];
+        uint32_t qa[RW][4], qb[RW][4], qh[RW][4];
+        float sc[RW][4], dd[RW];
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r) {
+        for (int r = 0; r < RW; ++r) {
             const uint8_t* blk = row[r] + (size_t)b * 210;
             uint32_t scw[2];
             ld_words_a2<4, LDS>(blk + 64 * h + 16 * k, qa[r]);
@@ -194,14 +195,14 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         // two high bits from bits 2g..2g+1 of each qh byte.  The quants go to
         // float unbiased (v_cvt_f32_ubyte) and the -32 is applied once per
         // group through the group's sum of x, which every row shares.
-        float G[kQmvRows][T][4], XS[T][4];
+        float G[RW][T][4], XS[T][4];
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 XS[t][g] = 0.f;
 #pragma unroll
-                for (int r = 0; r < kQmvRows; ++r) G[r][t][g] = 0.f;
+                for (int r = 0; r < RW; ++r) G[r][t][g] = 0.f;
             }
 #pragma unroll
         for (int l4 = 0; l4 < 4; ++l4) {  // l = 16k + 4*l4 .. +3
@@ -214,7 +215,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
                     XS[t][g] += (xv[g][0] + xv[g][1]) + (xv[g][2] + xv[g][3]);
                 }
 #pragma unroll
-                for (int r = 0; r < kQmvRows; ++r) {
+                for (int r = 0; r < RW; ++r) {
                     const uint32_t wa = qa[r][l4], wb = qb[r][l4], hh = qh[r][l4];
                     const uint32_t qw[4] = {
                         (wa & 0x0F0F0F0Fu) | ((hh << 4) & 0x30303030u),
@@ -229,7 +230,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             }
         }
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r)
+        for (int r = 0; r < RW; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 float sub = 0.f;
@@ -255,7 +256,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
             X1[t] = s1;
         }
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r) {
+        for (int r = 0; r < RW; ++r) {
             const uint8_t* p = row[r] + (size_t)68 * uw;
             uint32_t wds[17];
 #pragma unroll
@@ -292,7 +293,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[kQmvRows], 
         const int u = uw;
         const float* xc = xs + 64 * ux;
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r) {
+        for (int r = 0; r < RW; ++r) {
             float wv[64];
             if constexpr (TY == kF32) {
                 const float* p = reinterpret_cast<const float*>(row[r]) + 64 * u;
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_kernel(QmvArgs a) {
         for (int r = 0; r < kQmvRows; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
-        for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false>(row, u, u, xs, a.in_dim, acc);
+        for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false, kQmvRows>(row, u, u, xs, a.in_dim, acc);
 #pragma unroll
         for (int r = 0; r < kQmvRows; ++r) {
 #pragma unroll
@@ -397,7 +398,7 @@ template <> struct QChunk<kQ4K> { static constexpr int upg = 4, gbytes = 144, ni
 template <> struct QChunk<kQ6K> { static constexpr int upg = 4, gbytes = 210, ni = 4; };
 template <> struct QChunk<kQ8_0> { static constexpr int upg = 1, gbytes = 68, ni = 5; };
 template <int TY>
-constexpr size_t qmv_slice_bytes() { return (size_t)kQmvRows * QChunk<TY>::ni * 1024; }
+constexpr size_t qmv_slice_bytes() { return (size_t)kQmvLdsRows * QChunk<TY>::ni * 1024; }
 
 template <int TY, int T>
 __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) {
@@ -413,32 +414,32 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) 
     __syncthreads();
     uint8_t* slice = reinterpret_cast<uint8_t*>(xs + a.n_tok * a.in_dim) + wave * qmv_slice_bytes<TY>();
 
-    const int n_groups = (a.rows + kQmvRows - 1) / kQmvRows;
+    const int n_groups = (a.rows + kQmvLdsRows - 1) / kQmvLdsRows;
     const int n_units = a.in_dim / QTraits<TY>::unit;
     const int n_chunks = (n_units + 63) / 64;
     for (int g = blockIdx.x * kQmvWaves + wave; g < n_groups; g += gridDim.x * kQmvWaves) {
-        const int r0 = g * kQmvRows;
-        float acc[kQmvRows][T];
+        const int r0 = g * kQmvLdsRows;
+        float acc[kQmvLdsRows][T];
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r)
+        for (int r = 0; r < kQmvLdsRows; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
-        if (r0 + kQmvRows >= a.rows) {
+        if (r0 + kQmvLdsRows >= a.rows) {
             // the group with the matrix's last row: direct reads, exact bytes
-            const uint8_t* row[kQmvRows];
+            const uint8_t* row[kQmvLdsRows];
 #pragma unroll
-            for (int r = 0; r < kQmvRows; ++r) {
+            for (int r = 0; r < kQmvLdsRows; ++r) {
                 const int rr = r0 + r < a.rows ? r0 + r : r0;
                 row[r] = a.w + (size_t)rr * a.row_bytes;
             }
-            for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false>(row, u, u, xs, a.in_dim, acc);
+            for (int u = lane; u < n_units; u += 64) unit_dot<TY, T, false, kQmvLdsRows>(row, u, u, xs, a.in_dim, acc);
         } else {
             for (int c = 0; c < n_chunks; ++c) {
                 const int cu = min(64, n_units - 64 * c);  // units in this chunk
                 const size_t len = (size_t)(cu / UPG) * GB;
-                const uint8_t* lrow[kQmvRows];
+                const uint8_t* lrow[kQmvLdsRows];
 #pragma unroll
-                for (int r = 0; r < kQmvRows; ++r) {
+                for (int r = 0; r < kQmvLdsRows; ++r) {
                     const size_t s0 = (size_t)(r0 + r) * a.row_bytes + (size_t)c * CB;
                     const size_t w0 = s0 & ~(size_t)15;
                     const int n16 = (int)((s0 + len - w0 + 15) / 16);
@@ -453,11 +454,11 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) 
                     lrow[r] = dst + (s0 - w0);
                 }
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slice holds the chunk
-                if (lane < cu) unit_dot<TY, T, true>(lrow, lane, 64 * c + lane, xs, a.in_dim, acc);
+                if (lane < cu) unit_dot<TY, T, true, kQmvLdsRows>(lrow, lane, 64 * c + lane, xs, a.in_dim, acc);
             }
         }
 #pragma unroll
-        for (int r = 0; r < kQmvRows; ++r) {
+        for (int r = 0; r < kQmvLdsRows; ++r) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const float sum = wave_sum64(acc[r][t]);
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) 
 
 template <int TY>
 static lmx_status launch_lds(const QmvArgs& a, int T, hipStream_t st) {
-    const long groups = (a.rows + kQmvRows - 1) / kQmvRows;
+    const long groups = (a.rows + kQmvLdsRows - 1) / kQmvLdsRows;
     const long wgs = std::min<long>((groups + kQmvWaves - 1) / kQmvWaves, kQmvMaxWgs);
     const dim3 grid((unsigned)wgs);
     const size_t lds = (size_t)T * a.in_dim * sizeof(float) + kQmvWaves * qmv_slice_bytes<TY>();

@@ -62,9 +62,10 @@ def test_odd_q6k_block_count_per_row():
 
 
 @pytest.mark.parametrize("name", ["q4_k", "q6_k", "q8_0"])
-@pytest.mark.parametrize("rows,in_dim,n_tok", [(70, 2560, 1), (41, 12544, 3)])
+@pytest.mark.parametrize("rows,in_dim,n_tok", [(70, 2560, 1), (41, 6400, 1), (41, 12544, 3)])
 def test_partial_and_multiple_chunks(name, rows, in_dim, n_tok):
-    # rows staged through LDS in 64-unit chunks: 40 units (one partial chunk)
-    # and 196 units (three full chunks and a 4-unit one); odd Q6_K blocks per
-    # row put the chunks' windows at every 2-byte offset mod 16
-    run(name, rows, in_dim, n_tok, seed=11 + rows)
+    # Q6_K and Q8_0 rows staged through LDS in 64-unit chunks: 40 units (one
+    # partial chunk), 100 units (a full and a partial one) and 196 units
+    # (three full chunks and a 4-unit one); odd Q6_K blocks per row put the
+    # chunks' windows at every 2-byte offset mod 16.
+    run(name, rows, in_dim, n_tok, seed=11 + rows + n_tok)
