@@ -97,6 +97,23 @@ def bench_decode_headline(lmx, torch, steps, warmup):
     return ms, gbs, nbytes
 
 
+def bench_decode_c1(lmx, torch, steps=360, warmup=36):
+    """C1: batch 1, H=16, Hkv=8, hd=128, 512 cached f16 tokens, fp32 q, query
+    at position 511; 36 rotated layer caches.  Latency-bound: 2.1 MB a call."""
+    Hq, n, n_layers = 16, 512, N_LAYERS
+    ks = [torch.randn((n, HKV * HD), dtype=torch.float16, device="cuda") for _ in range(n_layers)]
+    vs = [torch.randn((n, HKV * HD), dtype=torch.float16, device="cuda") for _ in range(n_layers)]
+    q = torch.randn((1, Hq * HD), dtype=torch.float32, device="cuda")
+    out = torch.empty((1, Hq * HD), dtype=torch.float32, device="cuda")
+    ws = lmx.Workspace()
+    fns = [(lambda i=i: lmx.attention(q, ks[i], vs[i], n_heads=Hq, n_kv_heads=HKV, head_dim=HD,
+                                      base_pos=n - 1, out=out, workspace=ws)) for i in range(n_layers)]
+    ms = time_calls(fns, steps, warmup, torch)
+    nbytes = decode_bytes([n], Hq)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ctx": n, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 # -------------------------------------------------------------------- extras --
 def bench_decode_batched(lmx, torch, B, seed, steps=20, warmup=3):
     g = torch.Generator().manual_seed(seed)
@@ -340,14 +357,15 @@ def main():
     extra = {}
     if args.only == "all":
         for name, fn in [
+            ("decode_c1_ctx512", lambda: bench_decode_c1(lmx, torch)),
             ("decode_b8", lambda: bench_decode_batched(lmx, torch, 8, 8)),
             ("decode_b32", lambda: bench_decode_batched(lmx, torch, 32, 32)),
             ("gemma_decode_swa_w1024", lambda: bench_gemma_decode(lmx, torch, 1024)),
             ("gemma_decode_global", lambda: bench_gemma_decode(lmx, torch, 0)),
-            ("prefill_s512", lambda: bench_prefill(lmx, torch, 512)),
+            ("prefill_s512", lambda: bench_prefill(lmx, torch, 512, steps=50, warmup=5)),
             ("prefill_s2048", lambda: bench_prefill(lmx, torch, 2048)),
             ("prefill_s8192", lambda: bench_prefill(lmx, torch, 8192, steps=5, warmup=1)),
-            ("prefill_chunk512_on_4k", lambda: bench_prefill(lmx, torch, 512, base=4096)),
+            ("prefill_chunk512_on_4k", lambda: bench_prefill(lmx, torch, 512, base=4096, steps=50, warmup=5)),
             ("gemma_prefill_swa_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,
                                                            window=1024, scale=1 / 16, steps=5, warmup=1)),
             ("gemma_prefill_global_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,

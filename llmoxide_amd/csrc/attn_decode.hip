@@ -32,13 +32,17 @@ static long env_long(const char* name, long dflt) {
 // Workgroups the heuristic aims for, and the fewest tiles a wave should get
 // before a unit is split further.  One query row: one 4-wave workgroup per
 // CU on 256 CUs, all of them streaming at once.  Several rows (a batch of
-// sequences of unequal length): eight per CU, so that CUs whose workgroups
-// end early pick up queued ones (measured at B = 8 and 32: 2048 beats 256 by
-// 20% and 8%).  LMX_DECODE_TARGET_WGS / LMX_DECODE_MIN_TILES override them
-// for tuning sweeps.
+// sequences of unequal length): 256 per row and at least eight per CU, so
+// that CUs whose workgroups end early pick up queued ones.  Measured on
+// ragged 1k-32k batches of Qwen3-8B shape: at B = 8, 2048 beats 256 by 20%
+// and 4096 by 6%; at B = 32, 8192 beats 2048 by 28% (500 -> 359 us) and
+// 16384 by 5%.  Both optima give a 32k sequence 16-tile waves, as B = 1
+// has.  LMX_DECODE_TARGET_WGS / LMX_DECODE_MIN_TILES override them for
+// tuning sweeps.
 static long target_wgs(int n_q) {
     static long v = env_long("LMX_DECODE_TARGET_WGS", 0);
-    return v > 0 ? v : (n_q > 1 ? 2048 : 256);
+    if (v > 0) return v;
+    return n_q > 1 ? std::max(2048L, 256L * n_q) : 256;
 }
 static long min_tiles_per_wave() {
     static long v = env_long("LMX_DECODE_MIN_TILES", 2);

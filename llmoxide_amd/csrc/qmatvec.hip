@@ -381,8 +381,10 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_kernel(QmvArgs a) {
 // The per-unit reads above give each lane 2-16 bytes at a stride of a block:
 // one load instruction touches 30-50 cache lines and every line is touched
 // again by the next field's load, which keeps the texture addresser busy and
-// holds the stream well below HBM rate.  Here a wave copies a chunk of 64
-// units of each of its RW rows (16 K-quant blocks, or 128 Q8_0 blocks) into
+// holds the stream well below HBM rate.  Here a wave takes groups of two rows
+// (fewer registers than the direct kernel's four, so more waves stream at
+// once: Q6_K 4096 x 12288 20.0 -> 16.7 us) and copies a chunk of 64
+// units of each row (16 K-quant blocks, or 128 Q8_0 blocks) into
 // its own LDS slice with contiguous 16-byte LDS-DMA loads (the 16-aligned
 // window around the chunk, 1 KB per instruction), then runs the same unit_dot
 // from LDS.  The slice is private to the wave, so a wait for its own loads
