@@ -171,6 +171,69 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
+// ---- split-bf16 operands (chunks of 32 and 64 tokens)
+//
+// The 16x16x32 bf16 MFMA runs 16 times the fp32 MFMA's FLOPs per cycle.
+// Each fp32 operand x is carried as hi = bf16(x) and lo = bf16(x - hi)
+// (round to nearest even both times), and a product a b is accumulated in
+// fp32 as lo_a hi_b + hi_a lo_b + hi_a hi_b: the dropped lo_a lo_b and the
+// rounding of lo leave a relative error near 2^-16 per product, against
+// 2^-8 for a single bf16 product (measured on the C5 shapes over 2048
+// tokens: 1e-5 of max|S| and of max|o|, where one f16 pass gives 6e-4).
+// The state and every accumulator stay fp32.
+//
+// Operand layout of v_mfma_f32_16x16x32_bf16, lane l = 16 lq + lr:
+//   A[i][k]: lane (i = lr) holds k = 8 lq + e, e = 0..7;  B[k][j] likewise
+//   with j = lr;  D as for the fp32 MFMA (rows 4 lq + r, column lr).
+// Contraction slot 8 lq + e of step s is mapped to index
+//   32 s + 16 (e / 4) + 4 lq + e % 4,
+// so a lane's eight operands are its own four-element groups of two
+// adjacent 16-wide tiles: D tiles feed the next product's B operand, and
+// fp32 rows give the A operand as two float4, with no shuffle.
+//
+// A "piece" is one such operand for all 64 lanes: hi of lane l at byte
+// 16 l, lo at 1024 + 16 l (2 KiB).
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+struct Bf8 {
+    bf16x8 hi, lo;
+};
+constexpr int kPiece = 2048;
+
+__device__ __forceinline__ void split4(f32x4 x, bf16x4& hi, bf16x4& lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const __bf16 h = (__bf16)x[e];
+        hi[e] = h;
+        lo[e] = (__bf16)(x[e] - (float)h);
+    }
+}
+__device__ __forceinline__ Bf8 split8(f32x4 x0, f32x4 x1) {
+    bf16x4 h0, l0, h1, l1;
+    split4(x0, h0, l0);
+    split4(x1, h1, l1);
+    return Bf8{__builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7),
+               __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7)};
+}
+__device__ __forceinline__ Bf8 join8(bf16x4 h0, bf16x4 h1, bf16x4 l0, bf16x4 l1) {
+    return Bf8{__builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7),
+               __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7)};
+}
+__device__ __forceinline__ Bf8 ld_piece(const uint8_t* p, int lane) {
+    return Bf8{*reinterpret_cast<const bf16x8*>(p + 16 * lane),
+               *reinterpret_cast<const bf16x8*>(p + 1024 + 16 * lane)};
+}
+__device__ __forceinline__ void st_piece(uint8_t* p, int lane, const Bf8& v) {
+    *reinterpret_cast<bf16x8*>(p + 16 * lane) = v.hi;
+    *reinterpret_cast<bf16x8*>(p + 1024 + 16 * lane) = v.lo;
+}
+// c + a b over one 32-wide contraction step, both operands split.
+__device__ __forceinline__ f32x4 mfma3(const Bf8& a, const Bf8& b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, c, 0, 0, 0);
+}
+
 // Per-chunk inputs of a scan wave that are not K or Q (see the scan kernel).
 template <int NM>
 struct ChunkIn {
@@ -190,10 +253,15 @@ struct ChunkSmem {
 // once, into registers, from K and Q rows staged in LDS with whole-line loads;
 // the decays, the solve and M are per v-head, in LDS that reuses the staging
 // space.  Decays are handled in log2 units (exp2 is the native instruction).
-template <int SD, int C>
+//
+// SPLIT (chunks of 32 and 64): Tb and M go out as split-bf16 pieces, and the
+// chunk's K and Q are written once more, split, in the scan's operand order
+// (K and Q rows for X and Y, K^T for the state update) to ws_K, so the 16
+// scan workgroups that read a k-head's chunk split nothing themselves.
+template <int SD, int C, bool SPLIT>
 __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
                                                                float* ws_P, float* ws_e,
-                                                               int n_chunks) {
+                                                               uint8_t* ws_K, int n_chunks) {
     constexpr int NM = C / 16, LD = ChunkSmem<C>::LD;
     constexpr int NTILE = NM * (NM + 1) / 2, TPW = (NTILE + 3) / 4;
     constexpr int KLD = SD + 4;            // staged K/Q row stride in floats
@@ -266,6 +334,33 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
                 gk[k] = mfma4(a4[r], b4[r], gk[k]);
                 gq[k] = mfma4(q4[r], b4[r], gq[k]);
             }
+        }
+    }
+
+    if constexpr (SPLIT) {
+        // K, Q pieces (token tile m, dim step sg): lane (lr, lq) row 16 m + lr,
+        // dims 32 sg + 4 lq + {0..3} and + 16.  K^T pieces (dim tile ct, token
+        // step sg): lane (lr, lq) dim 16 ct + lr, tokens 32 sg + 4 lq + {0..3}
+        // and + 16.  Staged rows past the chunk's end are zero.
+        constexpr int SX = SD / 32, SC = C / 32;
+        uint8_t* kb = ws_K + ((size_t)ch * a.n_kh + hk) * (3 * C * SD * 4);
+        for (int q = tid; q < NM * SX * 64; q += 256) {
+            const int l = q & 63, pc = q >> 6, m = pc / SX, sg = pc % SX;
+            const int t = 16 * m + (l & 15), c0 = 32 * sg + 4 * (l >> 4);
+            st_piece(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)));
+            st_piece(kb + C * SD * 4 + pc * kPiece, l,
+                     split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)));
+        }
+        for (int q = tid; q < (SD / 16) * SC * 64; q += 256) {
+            const int l = q & 63, pc = q >> 6, ct = pc / SC, sg = pc % SC;
+            const int d = 16 * ct + (l & 15), t0 = 32 * sg + 4 * (l >> 4);
+            f32x4 x0, x1;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                x0[r] = Ks[(t0 + r) * KLD + d];
+                x1[r] = Ks[(t0 + 16 + r) * KLD + d];
+            }
+            st_piece(kb + 2 * C * SD * 4 + pc * kPiece, l, split8(x0, x1));
         }
     }
 
@@ -368,6 +463,32 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
             for (int r = 0; r < 4; ++r) As[(16 * m + 4 * lq + r) * LD + 16 * n + lr] = acc[r];
         }
         __syncthreads();
+        if constexpr (SPLIT) {
+            // Tb and M as split pieces (row tile bm, token step sg): lane
+            // (lr, lq) row 16 bm + lr, columns 32 sg + 4 lq + {0..3} and + 16.
+            // Entries above the diagonal (Tb) or in blocks above it (M) are 0.
+            constexpr int SC = C / 32;
+            uint8_t* Tg = reinterpret_cast<uint8_t*>(ws_T + cb * C * C);
+            uint8_t* Mg = reinterpret_cast<uint8_t*>(ws_P + cb * C * C);
+            for (int q = tid; q < NM * SC * 64; q += 256) {
+                const int l = q & 63, pc = q >> 6, bm = pc / SC, sg = pc % SC;
+                const int t = 16 * bm + (l & 15);
+                f32x4 to[2], mo[2];
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int i0 = 32 * sg + 16 * hf + 4 * (l >> 4), bn = 2 * sg + hf;
+                    const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        to[hf][e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
+                        mo[hf][e] = bn <= bm ? mv[e] : 0.f;
+                    }
+                }
+                st_piece(Tg + pc * kPiece, l, split8(to[0], to[1]));
+                st_piece(Mg + pc * kPiece, l, split8(mo[0], mo[1]));
+            }
+            continue;
+        }
         // Tb and M go out in MFMA A-operand order: block (m, n), lane
         // l = 16 lq + lr, element e holds row 16 m + lr, column 16 n + 4 lq + e,
         // so each lane of a scan wave reads its block with one float4 and the
@@ -596,9 +717,215 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(DeltaArgs a, cons
     for (int j = 0; j < TPW; ++j) *reinterpret_cast<f32x4*>(srow + 16 * (TPW * w + j)) = Sown[j];
 }
 
+// The scan on split-bf16 operands (chunks of 32 and 64 tokens): the same
+// work split and chunk algebra as delta_chunk_scan_kernel, every product a
+// 16x16x32 bf16 MFMA triple (mfma3).  K, Q, K^T, Tb and M arrive as pieces
+// from the prep kernel; the three operands formed here (Z, W = U exp(lg_C -
+// lg), and the updated state columns) are split once by the wave that
+// produces them and pass through LDS as bf16 hi/lo tiles in the D layout.
+// Each wave keeps its own state columns in fp32 (Sown) for the decay term
+// and the final store.  A piece register is reloaded with the next chunk's
+// piece right after its last use in this chunk.
+template <int SD, int C>
+__global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, const uint8_t* ws_T,
+                                                                  const uint8_t* ws_P,
+                                                                  const float* ws_e,
+                                                                  const uint8_t* ws_K, int n_chunks) {
+    constexpr int NT = SD / 16, NM = C / 16, TPW = NT / 4;
+    constexpr int SX = SD / 32, SC = C / 32;  // 32-wide steps over dims, over tokens
+    constexpr size_t KQB = (size_t)3 * C * SD * 4;  // ws_K bytes per (chunk, k-head)
+    static_assert(NM % 2 == 0 && NT % 4 == 0, "whole 32-wide steps, whole column tiles per wave");
+    __shared__ bf16x4 Zh[NM * 64], Zl[NM * 64];  // Z tiles, D layout
+    __shared__ bf16x4 Wh[NM * 64], Wl[NM * 64];  // W tiles, D layout
+    __shared__ bf16x4 Sh[NT * 64], Sl[NT * 64];  // state columns, D layout
+    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hv = blockIdx.x % a.n_vh, rb = blockIdx.x / a.n_vh;
+    const int row0 = rb * 16, hk = hv % a.n_kh;
+    const bool tok_wave = NM >= 4 || w < NM;
+    const int m = tok_wave ? w : 0;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    int vzero;  // a zero the compiler cannot see through (keeps gam on the vector path)
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+
+    // Row j = row0 + lr of S; Sown[jj] holds columns 16 (TPW w + jj) + 4 lq + r.
+    float* srow = a.state + ((size_t)hv * SD + row0 + lr) * SD + 4 * lq;
+    f32x4 Sown[TPW];
+#pragma unroll
+    for (int jj = 0; jj < TPW; ++jj) Sown[jj] = ld4(srow + 16 * (TPW * w + jj));
+    auto put_s = [&]() {
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj) {
+            bf16x4 h, l;
+            split4(Sown[jj], h, l);
+            Sh[(TPW * w + jj) * 64 + lane] = h;
+            Sl[(TPW * w + jj) * 64 + lane] = l;
+        }
+    };
+    Bf8 sb[SX];  // S^T as the B operand of X and Y
+    auto get_s = [&]() {
+#pragma unroll
+        for (int sg = 0; sg < SX; ++sg)
+            sb[sg] = join8(Sh[2 * sg * 64 + lane], Sh[(2 * sg + 1) * 64 + lane], Sl[2 * sg * 64 + lane],
+                           Sl[(2 * sg + 1) * 64 + lane]);
+    };
+
+    auto kq_base = [&](int ch) { return ws_K + ((size_t)ch * a.n_kh + hk) * KQB; };
+    auto mat_base = [&](const uint8_t* ws, int ch) { return ws + ((size_t)hv * n_chunks + ch) * (C * C * 4); };
+    Bf8 kx[SX], qx[SX], kt[TPW][SC], tb[SC], mm[SC];
+    auto ld_kx = [&](int ch, int sg) { kx[sg] = ld_piece(kq_base(ch) + (m * SX + sg) * kPiece, lane); };
+    auto ld_qx = [&](int ch, int sg) { qx[sg] = ld_piece(kq_base(ch) + C * SD * 4 + (m * SX + sg) * kPiece, lane); };
+    auto ld_kt = [&](int ch, int jj, int sg) {
+        kt[jj][sg] = ld_piece(kq_base(ch) + 2 * C * SD * 4 + ((TPW * w + jj) * SC + sg) * kPiece, lane);
+    };
+    auto ld_tb = [&](int ch, int sg) { tb[sg] = ld_piece(mat_base(ws_T, ch) + (m * SC + sg) * kPiece, lane); };
+    auto ld_mm = [&](int ch, int sg) { mm[sg] = ld_piece(mat_base(ws_P, ch) + (m * SC + sg) * kPiece, lane); };
+
+    // Small per-chunk inputs, two register sets (the loop is unrolled by two).
+    struct Small {
+        f32x4 v, e, wo;  // V, exp(lg), exp(lg_C - lg) at tokens 16 m + 4 lq + r
+        float gam;       // exp(lg_C)
+    };
+    // Tokens past the end of the last chunk read row 0 of the chunk instead:
+    // their b is 0, so their rows and columns of Tb are exactly zero and so
+    // are their U rows; only finiteness of what they read matters.
+    auto fetch_small = [&](int ch, Small& d) {
+        const float* eb = ws_e + ((size_t)hv * n_chunks + ch) * 2 * C;
+        d.gam = eb[C - 1 + vzero];
+        if (tok_wave) {
+            d.e = ld4(eb + 16 * m + 4 * lq);
+            d.wo = ld4(eb + C + 16 * m + 4 * lq);
+            const float* vcol = a.conv + 2 * (size_t)a.key_dim + (size_t)hv * SD + row0 + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tv = 16 * m + 4 * lq + r;
+                d.v[r] = vcol[(size_t)(ch * C + (tv < a.n_tok - ch * C ? tv : 0)) * a.conv_dim];
+            }
+        }
+    };
+
+    auto step = [&](int ch, const Small& cur, Small& nxt) {
+        const int nv = a.n_tok - ch * C;
+        const int cn = min(ch + 1, n_chunks - 1);
+        fetch_small(cn, nxt);
+        f32x4 X = z4, Y = z4;
+        if (tok_wave) {
+            // X = K S^T, Y = Q S^T over the dims
+#pragma unroll
+            for (int sg = 0; sg < SX; ++sg) {
+                X = mfma3(kx[sg], sb[sg], X);
+                Y = mfma3(qx[sg], sb[sg], Y);
+                ld_kx(cn, sg);
+                ld_qx(cn, sg);
+            }
+            // Z = V - exp(lg) X
+            f32x4 Z;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Z[r] = cur.v[r] - cur.e[r] * X[r];
+            bf16x4 h, l;
+            split4(Z, h, l);
+            Zh[m * 64 + lane] = h;
+            Zl[m * 64 + lane] = l;
+        }
+        __syncthreads();  // Z complete
+
+        if (tok_wave) {
+            // U = Tb Z and O = exp(lg) Y + M Z over the chunk's tokens
+            f32x4 U = z4, O;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) O[r] = cur.e[r] * Y[r];
+#pragma unroll
+            for (int sg = 0; sg < SC; ++sg) {
+                const Bf8 zb = join8(Zh[2 * sg * 64 + lane], Zh[(2 * sg + 1) * 64 + lane],
+                                     Zl[2 * sg * 64 + lane], Zl[(2 * sg + 1) * 64 + lane]);
+                U = mfma3(tb[sg], zb, U);
+                O = mfma3(mm[sg], zb, O);
+                ld_tb(cn, sg);
+                ld_mm(cn, sg);
+            }
+            float* orow = a.out + (size_t)ch * C * a.d_inner + (size_t)hv * SD + row0 + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * m + 4 * lq + r;
+                if (t < nv) orow[(size_t)t * a.d_inner] = O[r] * a.scale;
+            }
+            f32x4 W;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) W[r] = U[r] * cur.wo[r];
+            bf16x4 h, l;
+            split4(W, h, l);
+            Wh[m * 64 + lane] = h;
+            Wl[m * 64 + lane] = l;
+        }
+        __syncthreads();  // W complete
+
+        // S <- exp(lg_C) S + W^T K on this wave's columns
+        f32x4 acc[TPW];
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[jj][r] = cur.gam * Sown[jj][r];
+#pragma unroll
+        for (int sg = 0; sg < SC; ++sg) {
+            const Bf8 wb = join8(Wh[2 * sg * 64 + lane], Wh[(2 * sg + 1) * 64 + lane],
+                                 Wl[2 * sg * 64 + lane], Wl[(2 * sg + 1) * 64 + lane]);
+#pragma unroll
+            for (int jj = 0; jj < TPW; ++jj) {
+                acc[jj] = mfma3(kt[jj][sg], wb, acc[jj]);
+                ld_kt(cn, jj, sg);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj) Sown[jj] = acc[jj];
+        put_s();
+        __syncthreads();  // state columns complete
+        get_s();
+    };
+
+    // Chunk 0's inputs, drained before the loop so the waits inside it follow
+    // the loop body's own issue order.
+    Small in0, in1;
+    fetch_small(0, in0);
+    if (tok_wave) {
+#pragma unroll
+        for (int sg = 0; sg < SX; ++sg) {
+            ld_kx(0, sg);
+            ld_qx(0, sg);
+        }
+#pragma unroll
+        for (int sg = 0; sg < SC; ++sg) {
+            ld_tb(0, sg);
+            ld_mm(0, sg);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < TPW; ++jj)
+#pragma unroll
+        for (int sg = 0; sg < SC; ++sg) ld_kt(0, jj, sg);
+    put_s();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    get_s();
+    int ch = 0;
+    for (; ch + 1 < n_chunks; ch += 2) {
+        step(ch, in0, in1);
+        step(ch + 1, in1, in0);
+    }
+    if (ch < n_chunks) step(ch, in0, in1);
+#pragma unroll
+    for (int jj = 0; jj < TPW; ++jj) *reinterpret_cast<f32x4*>(srow + 16 * (TPW * w + jj)) = Sown[jj];
+}
+
+// Workspace: Tb and M [n_vh][n_chunks][chunk^2] floats (fp32 fragments, or
+// split-bf16 pieces of the same size), the decays [n_vh][n_chunks][2 chunk],
+// and, for the split path (chunks of 32 and 64), K, Q and K^T pieces
+// [n_chunks][n_kh][3 chunk s_dim] floats' worth.
+static bool chunk_split(int chunk) { return chunk >= 32; }
+
 static size_t chunk_ws_floats(const lmx_dop* op, int chunk) {
     const size_t n_chunks = (op->n_tok + chunk - 1) / chunk;
-    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk);
+    const size_t kq = chunk_split(chunk) ? (size_t)op->n_kh * n_chunks * 3 * chunk * op->s_dim : 0;
+    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk) + kq;
 }
 
 size_t deltanet_chunked_ws(const lmx_dop* op, int chunk) {
@@ -607,11 +934,17 @@ size_t deltanet_chunked_ws(const lmx_dop* op, int chunk) {
 
 template <int SD, int C>
 static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks, float* wsT,
-                           float* wsP, float* wsE, hipStream_t st) {
-    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C>), dim3(n_chunks, n_kh), dim3(256), 0, st, a,
-                       wsT, wsP, wsE, n_chunks);
-    hipLaunchKernelGGL((delta_chunk_scan_kernel<SD, C>), dim3(n_vh * (SD / 16)), dim3(256), 0, st,
-                       a, wsT, wsP, wsE, n_chunks);
+                           float* wsP, float* wsE, uint8_t* wsK, hipStream_t st) {
+    constexpr bool SPLIT = C >= 32;
+    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C, SPLIT>), dim3(n_chunks, n_kh), dim3(256), 0, st,
+                       a, wsT, wsP, wsE, wsK, n_chunks);
+    if constexpr (SPLIT)
+        hipLaunchKernelGGL((delta_chunk_scan_bf_kernel<SD, C>), dim3(n_vh * (SD / 16)), dim3(256), 0, st,
+                           a, reinterpret_cast<const uint8_t*>(wsT), reinterpret_cast<const uint8_t*>(wsP),
+                           wsE, wsK, n_chunks);
+    else
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<SD, C>), dim3(n_vh * (SD / 16)), dim3(256), 0, st,
+                           a, wsT, wsP, wsE, n_chunks);
 }
 
 lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* dt_bias,
@@ -625,11 +958,12 @@ lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* 
     float* wsT = static_cast<float*>(ws);
     float* wsP = wsT + per * chunk * chunk;
     float* wsE = wsP + per * chunk * chunk;
+    uint8_t* wsK = reinterpret_cast<uint8_t*>(wsE + per * 2 * chunk);
     const int sd = (int)op->s_dim;
     (void)hipGetLastError();
 #define LMX_CH(SDV, CV)                                                                          \
     if (sd == SDV && chunk == CV) {                                                              \
-        launch_chunked<SDV, CV>(a, (int)op->n_vh, (int)op->n_kh, n_chunks, wsT, wsP, wsE, st);    \
+        launch_chunked<SDV, CV>(a, (int)op->n_vh, (int)op->n_kh, n_chunks, wsT, wsP, wsE, wsK, st); \
         LMX_CHECK_LAUNCH();                                                                      \
         return LMX_OK;                                                                           \
     }
