@@ -255,7 +255,9 @@ lmx_status lmx_deltanet_recur(const lmx_dop *op, const float *ssm_a, const float
  * contract and results as lmx_deltanet_recur within the stated tolerance; the
  * reference has no chunked form (it runs the token loop in one workgroup per
  * head, deltanet.wgsl:175-239), so this is the prefill counterpart of the same
- * dispatch.  chunk: 64 (or 32, 16).
+ * dispatch.  chunk: 64 (or 32, 16).  Chunks of 32 and 64 form their products
+ * on bf16 matrix cores from split (hi + lo) operands with fp32 accumulation
+ * (about 1e-5 relative to fp32 products); the state stays fp32.
  */
 size_t lmx_deltanet_chunked_workspace_bytes(const lmx_dop *op, int32_t chunk);
 

@@ -149,8 +149,10 @@ lmx_status deltanet_recur(const lmx_dop* op, const float* ssm_a, const float* dt
 //
 // (M Z = P U; folding Tb into M lets O be formed from Z alongside U.)
 //
-// Every product runs on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), so
-// the arithmetic stays fp32 like the sequential form.  Kernel 1 (one
+// With chunks of 16 every product runs on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32); with chunks of 32 and 64 on the bf16 ones with
+// split operands (see "split-bf16 operands" below: about 2^-16 relative per
+// product, fp32 accumulation, the state kept in fp32).  Kernel 1 (one
 // workgroup per (chunk, k-head), all in parallel) builds Tb, M and the decay
 // vectors of every v-head that reads that k-head.  Kernel 2 (one workgroup
 // per (v-head, 16 state rows)) walks the chunks in order with its rows of S
