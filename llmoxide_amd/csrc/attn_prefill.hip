@@ -26,6 +26,8 @@
 
 #include "common.hpp"
 
+
+
 namespace lmx {
 
 struct PrefillArgs {
@@ -65,6 +67,45 @@ __device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
 
 // Bijective block remap so that consecutive logical ids share an XCD (blocks
 // are dispatched round-robin over 8 XCDs).
+// S^T - mb = K Q^T - mb for KB 32-key blocks of a K tile in LDS (rows of
+// KPAD halfs), Q^T in registers as the B operand.  The K operand reads run
+// QK_DEPTH ahead of the MFMAs (the compiler's own schedule kept one or two
+// in flight, so every MFMA waited out most of an LDS round trip); the
+// (k-step, block) order alternates the KB accumulator chains.  Depth 4 at
+// head_dim <= 128 (6 spills in the 128-row kernel), QK_DEPTH_HD256 at 256,
+// where one wave per SIMD has the registers (measured: depth 4 +2-3% at
+// S = 8192, +7% on Gemma hd 256 global 4k; depth 6 a further +2-3% there).
+#ifndef LMX_QK_DEPTH_HD256
+#define LMX_QK_DEPTH_HD256 8
+#endif
+template <int HD>
+constexpr int qk_depth() { return HD >= 256 ? LMX_QK_DEPTH_HD256 : 4; }
+template <int HD, int KB, int KPAD>
+__device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16], f32x16 (&s)[KB], float mb,
+                                        int l32, int hh) {
+    constexpr int KSTEPS = HD / 16, NQ = KSTEPS * KB;
+    constexpr int D = qk_depth<HD>() < NQ ? qk_depth<HD>() : NQ;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
+    auto rd = [&](int q) {
+        const int ks = q / KB, kb = q % KB;
+        return *reinterpret_cast<const f16x8*>(&Ks[(kb * 32 + l32) * KPAD + 8 * hh + ks * 16]);
+    };
+    f16x8 ka[NQ];
+#pragma unroll
+    for (int q = 0; q < D; ++q) ka[q] = rd(q);
+    __builtin_amdgcn_sched_group_barrier(0x100, D, 0);  // the first D reads
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        if (q + D < NQ) ka[q + D] = rd(q + D);
+        s[q % KB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[q], qf[q / KB], s[q % KB], 0, 0, 0);
+        if (q + D < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+    }
+}
+
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
     const int q = n / 8, r = n % 8;
     const int xcd = bid % 8, local = bid / 8;
@@ -275,17 +316,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         //      come out already shifted for exp2.
         float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
-            const f16* krow = &Ks[(kb * 32 + l32) * KPAD + 8 * hh];
-#pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + ks * 16);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[ks], s[kb], 0, 0, 0);
-            }
-        }
+        qk_tile<HD, KB, KPAD>(Ks, qf, s, mb, l32, hh);
 
         // ---- mask, online softmax.  s[kb][i] is key
         //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
@@ -662,17 +693,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     // S^T - mb = K Q^T - mb; mb is the running max once one is set.
     auto qk = [&](const f16* Ks) {
         mb = m_run > -1e29f ? m_run : 0.f;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                const f16x8 ka = *reinterpret_cast<const f16x8*>(&Ks[(kb * 32 + l32) * KPAD + 8 * hh + ks * 16]);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[ks], s[kb], 0, 0, 0);
-            }
+        qk_tile<HD, KB, KPAD>(Ks, qf, s, mb, l32, hh);
     };
     // s[kb][i] is key kt + 32*kb + 8*(i/4) + 4*hh + i%4 of query qrow.
     auto mask = [&](int kt) {
