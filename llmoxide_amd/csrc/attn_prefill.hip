@@ -52,6 +52,7 @@ struct PrefillArgs {
 };
 
 constexpr int kPfBM = 128;  // query rows per workgroup
+constexpr int kPfCus = 256;  // compute units of the target (MI355X)
 // Keys per LDS tile: 64, or 32 at head_dim >= 256 (the register prefetch of
 // the next tile and the o accumulators share one register file).
 template <int HD>
@@ -131,7 +132,14 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     const int per_kvh = a.n_qtiles * a.G * n_split;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
-    const int qt = a.n_qtiles - 1 - rem / (a.G * n_split);
+    // Query tiles heaviest first (causal work grows with qt).  When the whole
+    // grid is resident at once (two workgroups per CU), the second half is
+    // walked lightest first, so the two workgroups a CU receives pair a heavy
+    // tile with a light one instead of two of nearly the same weight.
+    const int pos = rem / (a.G * n_split);
+    const int half = (a.n_qtiles + 1) / 2;
+    const bool fold = HD <= 128 && nblk <= 2 * kPfCus;
+    const int qt = (fold && pos >= half) ? pos - half : a.n_qtiles - 1 - pos;
     const int rem2 = rem % (a.G * n_split);
     const int h = kvh * a.G + rem2 / n_split;
     const int sp = rem2 % n_split;
