@@ -37,12 +37,14 @@ static long env_long(const char* name, long dflt) {
 // ragged 1k-32k batches of Qwen3-8B shape: at B = 8, 2048 beats 256 by 20%
 // and 4096 by 6%; at B = 32, 8192 beats 2048 by 28% (500 -> 359 us) and
 // 16384 by 5%.  Both optima give a 32k sequence 16-tile waves, as B = 1
-// has.  LMX_DECODE_TARGET_WGS / LMX_DECODE_MIN_TILES override them for
-// tuning sweeps.
+// has.  The target stops growing at 16384 (B = 64), which bounds the split
+// partials, and so the workspace, for large batches (B = 256 at 32k: 136 MB
+// rather than 545 MB).  LMX_DECODE_TARGET_WGS / LMX_DECODE_MIN_TILES
+// override them for tuning sweeps.
 static long target_wgs(int n_q) {
     static long v = env_long("LMX_DECODE_TARGET_WGS", 0);
     if (v > 0) return v;
-    return n_q > 1 ? std::max(2048L, 256L * n_q) : 256;
+    return n_q > 1 ? std::max(2048L, std::min(16384L, 256L * n_q)) : 256;
 }
 static long min_tiles_per_wave() {
     static long v = env_long("LMX_DECODE_MIN_TILES", 2);
