@@ -174,6 +174,33 @@ def test_deltanet_validation():
     assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), 48) == 0
 
 
+@pytest.mark.parametrize("T,n_vh,n_kh,sd", [(4096, 32, 16, 128), (37, 4, 2, 64), (200, 8, 4, 128)])
+def test_deltanet_chunked_workspace_size(T, n_vh, n_kh, sd):
+    # per (v-head, chunk): Tb and M (chunk^2 floats each) and the decays (2 chunk);
+    # chunks of 32 and 64 add the split-bf16 K, Q and K^T of every (chunk, k-head),
+    # 3 * chunk * s_dim floats' worth; all rounded up to 256 bytes
+    L = lmx.lib()
+    op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    for chunk in (16, 32, 64):
+        n_ch = (T + chunk - 1) // chunk
+        floats = n_vh * n_ch * (2 * chunk * chunk + 2 * chunk)
+        if chunk >= 32:
+            floats += n_kh * n_ch * 3 * chunk * sd
+        want = (floats * 4 + 255) // 256 * 256
+        assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk) == want
+
+
+def test_batched_decode_workspace_stops_growing():
+    # the split target grows with the batch up to 16384 workgroups (B = 64 at
+    # Qwen3-8B shape), so the partials' workspace is bounded for large batches
+    L = lmx.lib()
+    p = _params(n_slots=32768)
+    ws = {B: L.lmx_attn_decode_batched_workspace_bytes(ctypes.byref(p), B, 32768) for B in (8, 32, 64, 256)}
+    assert ws[8] < ws[32] < ws[64]
+    assert ws[256] == ws[64]
+    assert ws[256] < 150_000_000
+
+
 def _pro(**kw):
     base = dict(n_tokens=4, n_heads=32, n_kv_heads=8, head_dim=128, q_stride=128, n_rot=128,
                 base_pos=0, window=0, n_slots=16, v_norm=0, rms_eps=1e-6, rope_base=1e6)

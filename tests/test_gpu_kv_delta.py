@@ -129,3 +129,18 @@ def test_batched_single_sequence_equals_attn_fwd():
     single = lmx.attention(dev(c.q), ks[0], vs[0], n_heads=32, n_kv_heads=8, head_dim=128,
                            base_pos=4999)
     assert np.array_equal(single.cpu().numpy(), out)
+
+
+def test_delta_chunked_c5_full_size_matches_sequential_kernel():
+    """C5 at full size (T=4096, 32 v-heads, 16 k-heads, d=128, chunk 64): the
+    chunked kernel (split-bf16 products) against the token-sequential fp32
+    kernel, which the oracle pins at smaller sizes; both outputs and the final
+    state within the attention tolerance."""
+    n_vh, n_kh, sd, T = 32, 16, 128, 4096
+    say(f"delta_chunked C5 full size T={T} n_vh={n_vh} n_kh={n_kh} vs delta_recur")
+    conv, al, be, S0, A, dt = delta_inputs(4099, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.0)
+    o_seq, S_seq = _delta_gpu(lmx.delta_recur, conv, al, be, S0, A, dt, n_vh, n_kh, sd)
+    o_chk, S_chk = _delta_gpu(lmx.delta_chunked, conv, al, be, S0, A, dt, n_vh, n_kh, sd, chunk=64)
+    e_o = assert_close(o_chk, o_seq, what="o")
+    e_s = assert_close(S_chk, S_seq, what="S")
+    say(f"  o max_abs={e_o[0]:.2e} rel={e_o[1]:.2e}; S max_abs={e_s[0]:.2e} rel={e_s[1]:.2e}")
