@@ -119,6 +119,13 @@ def test_batched_ragged_b8():
     _batched(8, rng.integers(1024, 32769, 8).tolist(), seed=100)
 
 
+def test_batched_ragged_b32():
+    # B = 32 takes the batch-scaled split target (8192 workgroups): 128 splits
+    # per unit at an 8k longest context, merged in 16 parts
+    rng = np.random.default_rng(32)
+    _batched(32, rng.integers(64, 8193, 32).tolist(), seed=400)
+
+
 def test_batched_small_and_f16_query():
     _batched(5, [1, 2, 64, 65, 700], seed=200, q_f16=True)
 
