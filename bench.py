@@ -8,14 +8,27 @@ step is one decode-attention call for one layer; the timed steps rotate over
 the KV bytes come from HBM, not from the 256 MB last-level cache.  Inputs are
 synthetic N(0,1), resident in HBM before timing starts.
 
-Timing: HIP events recorded on the stream the kernels are launched on, around
-exactly --steps calls after --warmup untimed calls, with device syncs on both
-sides.  ``roofline.achieved`` = algorithmic bytes per launch / mean launch time.
+Timing (every config):
+  * warm-up: at least --warmup calls and at least 0.3 s of them;
+  * timed region: HIP events recorded on the stream the kernels run on,
+    around exactly --steps calls, with device syncs on both sides.  A spin
+    kernel (torch.cuda._sleep) is queued just before the first event so the
+    host enqueues the calls while it runs: the events then time the GPU
+    executing the calls back to back, not the 8-10 us ctypes launch of each
+    call.  ``ms_per_step`` is the mean over the timed region;
+  * median: per-call events over a second pass of the same calls.
+``roofline.achieved`` = algorithmic bytes per call / mean time per call.
 
-Other configs (ragged batches, prefill, Gemma-shape, delta-net) are reported
-under ``extra`` with their own roofline fractions; they are not the headline.
-The CPU baseline is the C restatement of the reference's scalar loops
-(oracle/), timed on a bounded sample on this host, 1 thread.
+Other configs (C1, ragged batches, prefill, Gemma shape, delta-net, the f-row
+kernels) are reported under ``extra`` with their own roofline fractions and
+medians.  Prefill (C3) inputs follow the config recipe: N(0,1), per-head
+RMS norm of Q and K, then f16.
+
+CPU baseline: the C restatement of the reference's scalar loops (oracle/,
+cpu.rs:342-387 for attention, qwen35/cpu.rs:188-246 for the delta rule),
+compiled -O2 without fast-math, timed on this host on a bounded sample of
+each config, on one core (the reference's attention loop is serial) and on
+all the cores this process may use (threads over heads), up to 16.
 """
 from __future__ import annotations
 
@@ -36,6 +49,7 @@ METRIC = "decode-attn HBM GB/s (% peak) Qwen3-8B 32k ctx; prefill-attn TFLOP/s"
 H, HKV, HD = 32, 8, 128
 CTX = 32768
 N_LAYERS = 36
+WARM_S = 0.3
 
 
 def log(*a):
@@ -53,19 +67,61 @@ def prefill_flops(pairs, H=H, hd=HD):
     return 4 * hd * H * pairs
 
 
+def visible_pairs(S, base=0, window=0):
+    pairs = 0
+    for i in range(S):
+        pos = base + i
+        lo = max(0, pos - window + 1) if window else 0
+        pairs += pos - lo + 1
+    return pairs
+
+
+DELTA_BYTES_PER_TOKEN = (8192 + 2 * 32 + 4096) * 4  # conv row, alpha, beta in; out row
+DELTA_STATE_BYTES = 2 * 32 * 128 * 128 * 4          # S read and written
+
+
+def delta_bytes(T):
+    return DELTA_BYTES_PER_TOKEN * T + DELTA_STATE_BYTES
+
+
+# -------------------------------------------------------------------- timing --
+def _sleep_ahead(torch, n_calls):
+    """Queue a spin kernel long enough for the host to enqueue n_calls calls
+    (about 15 us each through ctypes) behind it."""
+    us = 2000 + 15 * n_calls
+    torch.cuda._sleep(int(us * 2400))  # cycles at up to 2.4 GHz
+
+
 def time_calls(fns, steps, warmup, torch):
-    """Mean ms per call of fns[i % len(fns)], HIP events on the current stream."""
-    for i in range(warmup):
-        fns[i % len(fns)]()
+    """Mean and median ms per call of fns[i % len(fns)] (see the module doc)."""
+    n = len(fns)
+    i, t0 = 0, time.perf_counter()
+    while i < warmup or time.perf_counter() - t0 < WARM_S:
+        fns[i % n]()
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _sleep_ahead(torch, steps)
     e0.record(st)
     for i in range(steps):
-        fns[i % len(fns)]()
+        fns[i % n]()
     e1.record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    mean = e0.elapsed_time(e1) / steps
+    # median over per-call intervals (a second pass; the events add a little)
+    m = min(steps, 200)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(m + 1)]
+    _sleep_ahead(torch, m)
+    ev[0].record(st)
+    for i in range(m):
+        fns[i % n]()
+        ev[i + 1].record(st)
+    torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(m))
+    return mean, per[m // 2]
 
 
 def read_traffic(name):
@@ -74,6 +130,16 @@ def read_traffic(name):
         return None
     with open(path) as f:
         return json.load(f).get("bytes_per_launch")
+
+
+def hbm_entry(nbytes, ms, med, **kw):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(kw, ms=ms, median_ms=med, bytes=nbytes, **{"GB/s": gbs}, frac_hbm=gbs / HBM_PEAK_GBS)
+
+
+def mfma_entry(flops, ms, med, **kw):
+    tfs = flops / (ms * 1e-3) / 1e12
+    return dict(kw, ms=ms, median_ms=med, flops=flops, **{"TFLOP/s": tfs}, frac_mfma=tfs / MFMA_F16_PEAK_TFS)
 
 
 # ------------------------------------------------------------------ headline --
@@ -89,17 +155,17 @@ def bench_decode_headline(lmx, torch, steps, warmup):
                                    base_pos=CTX - 1, out=out, workspace=ws))
         for i in range(n_layers)
     ]
-    ms = time_calls(fns, steps, warmup, torch)
+    ms, med = time_calls(fns, steps, warmup, torch)
     nbytes = decode_bytes([CTX])
-    gbs = nbytes / (ms * 1e-3) / 1e9
     del ks, vs
     torch.cuda.empty_cache()
-    return ms, gbs, nbytes
+    return ms, med, nbytes
 
 
+# -------------------------------------------------------------------- extras --
 def bench_decode_c1(lmx, torch, steps=360, warmup=36):
     """C1: batch 1, H=16, Hkv=8, hd=128, 512 cached f16 tokens, fp32 q, query
-    at position 511; 36 rotated layer caches.  Latency-bound: 2.1 MB a call."""
+    at position 511; 36 rotated layer caches.  2.1 MB a call."""
     Hq, n, n_layers = 16, 512, N_LAYERS
     ks = [torch.randn((n, HKV * HD), dtype=torch.float16, device="cuda") for _ in range(n_layers)]
     vs = [torch.randn((n, HKV * HD), dtype=torch.float16, device="cuda") for _ in range(n_layers)]
@@ -108,16 +174,18 @@ def bench_decode_c1(lmx, torch, steps=360, warmup=36):
     ws = lmx.Workspace()
     fns = [(lambda i=i: lmx.attention(q, ks[i], vs[i], n_heads=Hq, n_kv_heads=HKV, head_dim=HD,
                                       base_pos=n - 1, out=out, workspace=ws)) for i in range(n_layers)]
-    ms = time_calls(fns, steps, warmup, torch)
-    nbytes = decode_bytes([n], Hq)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"ctx": n, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    ms, med = time_calls(fns, steps, warmup, torch)
+    return hbm_entry(decode_bytes([n], Hq), ms, med, ctx=n)
 
 
-# -------------------------------------------------------------------- extras --
-def bench_decode_batched(lmx, torch, B, seed, steps=20, warmup=3):
+def ragged_lens(B, seed):
+    import torch
     g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(1024, CTX + 1, (B,), generator=g).tolist()
+    return torch.randint(1024, CTX + 1, (B,), generator=g).tolist()
+
+
+def bench_decode_batched(lmx, torch, B, seed, steps=20, warmup=3):
+    lens = ragged_lens(B, seed)
     max_ctx = max(lens)
     sets = []
     for _ in range(2):  # two independent cache sets, alternated
@@ -131,19 +199,29 @@ def bench_decode_batched(lmx, torch, B, seed, steps=20, warmup=3):
     fns = [(lambda s=s: lmx.attention_decode_batched(q, s, ctx, max_ctx=max_ctx, n_heads=H, n_kv_heads=HKV,
                                                      head_dim=HD, n_slots=max_ctx, out=out, workspace=ws))
            for s in sets]
-    ms = time_calls(fns, steps, warmup, torch)
-    nbytes = decode_bytes(lens)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"B": B, "sum_ctx": sum(lens), "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
-            "tokens/s": B / (ms * 1e-3)}
+    ms, med = time_calls(fns, steps, warmup, torch)
+    e = hbm_entry(decode_bytes(lens), ms, med, B=B, sum_ctx=sum(lens))
+    e["tokens/s"] = B / (ms * 1e-3)
+    return e
 
 
-def bench_prefill(lmx, torch, S, base=0, Hq=H, Hkv=HKV, hd=HD, window=0, scale=None, steps=10,
-                  warmup=2):
+def qk_normed_f16(torch, rows, heads, hd, eps=1e-6):
+    """C3 recipe: N(0,1), per-head RMS norm without gain (ops.rs:40-47), f16."""
+    x = torch.randn((rows, heads, hd), dtype=torch.float32, device="cuda")
+    x = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
+    return x.reshape(rows, heads * hd).to(torch.float16)
+
+
+def bench_prefill(lmx, torch, S, base=0, Hq=H, Hkv=HKV, hd=HD, window=0, scale=None, qk_norm=True,
+                  steps=10, warmup=2):
     n_pos = base + S
-    k = torch.randn((n_pos, Hkv * hd), dtype=torch.float16, device="cuda")
+    if qk_norm:
+        k = qk_normed_f16(torch, n_pos, Hkv, hd)
+        q = qk_normed_f16(torch, S, Hq, hd)
+    else:
+        k = torch.randn((n_pos, Hkv * hd), dtype=torch.float16, device="cuda")
+        q = torch.randn((S, Hq * hd), dtype=torch.float16, device="cuda")
     v = torch.randn((n_pos, Hkv * hd), dtype=torch.float16, device="cuda")
-    q = torch.randn((S, Hq * hd), dtype=torch.float16, device="cuda")
     out = torch.empty((S, Hq * hd), dtype=torch.float32, device="cuda")
     ws = lmx.Workspace()
     kw = {}
@@ -155,16 +233,11 @@ def bench_prefill(lmx, torch, S, base=0, Hq=H, Hkv=HKV, hd=HD, window=0, scale=N
         kw = dict(k_cur=k[base:], v_cur=v[base:])
     fn = lambda: lmx.attention(q, kc, vc, n_heads=Hq, n_kv_heads=Hkv, head_dim=hd, base_pos=base,
                                window=window, scale=scale, out=out, workspace=ws, **kw)
-    ms = time_calls([fn], steps, warmup, torch)
-    pairs = 0
-    for i in range(S):
-        pos = base + i
-        lo = max(0, pos - window + 1) if window else 0
-        pairs += pos - lo + 1
-    fl = prefill_flops(pairs, Hq, hd)
-    tfs = fl / (ms * 1e-3) / 1e12
-    return {"S": S, "base": base, "window": window, "ms": ms, "TFLOP/s": tfs,
-            "frac_mfma": tfs / MFMA_F16_PEAK_TFS, "tokens/s": S / (ms * 1e-3)}
+    ms, med = time_calls([fn], steps, warmup, torch)
+    e = mfma_entry(prefill_flops(visible_pairs(S, base, window), Hq, hd), ms, med, S=S, base=base,
+                   window=window, inputs="QK-normed" if qk_norm else "N(0,1)")
+    e["tokens/s"] = S / (ms * 1e-3)
+    return e
 
 
 def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5):
@@ -179,10 +252,8 @@ def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5):
     fns = [(lambda i=i: lmx.attention(q, ks[i], vs[i], n_heads=Hq, n_kv_heads=Hkv, head_dim=hd,
                                       base_pos=CTX - 1, window=window, scale=1 / 16, out=out, workspace=ws))
            for i in range(n_layers)]
-    ms = time_calls(fns, steps, warmup, torch)
-    nbytes = decode_bytes([min(window or CTX, CTX)], Hq, Hkv, hd)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"window": window, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    ms, med = time_calls(fns, steps, warmup, torch)
+    return hbm_entry(decode_bytes([min(window or CTX, CTX)], Hq, Hkv, hd), ms, med, window=window)
 
 
 def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
@@ -199,28 +270,26 @@ def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
     kg = torch.ones(hd, device="cuda")
     fn = lambda: lmx.attn_prologue(q, k, v, kc, vc, n_heads=H, n_kv_heads=Hkv, head_dim=hd,
                                    base_pos=0, q_gain=qg, k_gain=kg)
-    ms = time_calls([fn], steps, warmup, torch)
-    nbytes = t * (H * hd * 8 + 2 * kv_dim * 4 + 2 * kv_dim * 2)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"t": t, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    ms, med = time_calls([fn], steps, warmup, torch)
+    return hbm_entry(t * (H * hd * 8 + 2 * kv_dim * 4 + 2 * kv_dim * 2), ms, med, t=t)
 
 
-def bench_matvec(lmx, torch, qtype, rows, in_dim, n_mats, steps=50, warmup=5):
-    """lmx_matvec at one token: y = W x over n_mats distinct weight matrices in
-    turn (so W comes from HBM, as a decode step's projections do).  Bytes are
-    the weight bytes (x and y are 4 * (in_dim + rows))."""
+def bench_matvec(lmx, torch, qtype, rows, in_dim, n_mats, n_tok=1, steps=50, warmup=5):
+    """lmx_matvec: y = W x over n_mats distinct weight matrices in turn (so W
+    comes from HBM, as a decode step's projections do).  Bytes are the weight
+    bytes plus x and y."""
     bb, be = {"q4_k": (144, 256), "q6_k": (210, 256), "q8_0": (34, 32), "bf16": (2, 1)}[qtype]
     nbytes = rows * (in_dim // be) * bb
     ws = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(n_mats)]
-    x = torch.randn((1, in_dim), device="cuda")
-    y = torch.empty((1, rows), device="cuda")
+    x = torch.randn((n_tok, in_dim), device="cuda")
+    y = torch.empty((n_tok, rows), device="cuda")
     fns = [(lambda w=w: lmx.matvec(w, x, qtype=qtype, rows=rows, in_dim=in_dim, y=y)) for w in ws]
-    ms = time_calls(fns, steps, warmup, torch)
-    total = nbytes + 4 * (in_dim + rows)
-    gbs = total / (ms * 1e-3) / 1e9
+    ms, med = time_calls(fns, steps, warmup, torch)
     del ws
-    return {"type": qtype, "rows": rows, "in_dim": in_dim, "weight_bytes": nbytes, "ms": ms,
-            "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    e = hbm_entry(nbytes + 4 * n_tok * (in_dim + rows), ms, med, type=qtype, rows=rows, in_dim=in_dim,
+                  n_tok=n_tok, weight_bytes=nbytes)
+    e["TFLOP/s"] = 2.0 * rows * in_dim * n_tok / (ms * 1e-3) / 1e12
+    return e
 
 
 def bench_kvm(lmx, torch, which, steps=20, warmup=3):
@@ -231,11 +300,10 @@ def bench_kvm(lmx, torch, which, steps=20, warmup=3):
     if which == "wipe":
         m = lmx.KvManager(layers, n_ctx=CTX, max_seqs=1)
         s = m.open()
-        ms = time_calls([lambda: m.wipe(s)], steps, warmup, torch)
+        ms, med = time_calls([lambda: m.wipe(s)], steps, warmup, torch)
         nbytes = m.arena_bytes
         del m
-        return {"bytes": nbytes, "ms": ms, "GB/s": nbytes / (ms * 1e-3) / 1e9,
-                "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        return hbm_entry(nbytes, ms, med)
     m = lmx.KvManager(layers, n_ctx=CTX, max_seqs=32, arena=(1 << 20, 1 << 48))
     seqs = [m.open() for _ in range(32)]
     for i, s in enumerate(seqs):
@@ -269,9 +337,8 @@ def bench_delta_io(lmx, torch, T, which, steps=20, warmup=3):
         w = torch.ones(sd, device="cuda")
         fn = lambda: lmx.delta_back(o, z, w, n_vh=n_vh, s_dim=sd)
         nbytes = 3 * T * d_inner * 4 + sd * 4
-    ms = time_calls([fn], steps, warmup, torch)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"T": T, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    ms, med = time_calls([fn], steps, warmup, torch)
+    return hbm_entry(nbytes, ms, med, T=T)
 
 
 def bench_delta(lmx, torch, T, chunked, steps=5, warmup=1):
@@ -292,36 +359,145 @@ def bench_delta(lmx, torch, T, chunked, steps=5, warmup=1):
                                        chunk=64, out=out, workspace=ws)
     else:
         fn = lambda: lmx.delta_recur(conv, al, be, state, A, dt, n_vh=n_vh, n_kh=n_kh, s_dim=sd, out=out)
-    ms = time_calls([fn], steps, warmup, torch)
-    nbytes = (conv_dim + 2 * n_vh + n_vh * sd) * 4 * T + 2 * n_vh * sd * sd * 4
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"T": T, "chunked": chunked, "ms": ms, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
-            "tokens/s": T / (ms * 1e-3)}
+    ms, med = time_calls([fn], steps, warmup, torch)
+    e = hbm_entry(delta_bytes(T), ms, med, T=T, chunked=chunked)
+    e["tokens/s"] = T / (ms * 1e-3)
+    return e
 
 
 # -------------------------------------------------------------- CPU baseline --
-def cpu_baseline(budget_s=12.0):
-    """The C restatement of the reference's scalar attention loop (cpu.rs:342-387;
-    qwen35/cpu.rs:324-365) on the headline shape, 1 thread, bounded sample."""
+def cpu_cores_all():
+    """Cores this process may use, at most 16 (one GPU's share of the box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+_KV_CACHE = {}
+
+
+def _cpu_kv(n_pos, kv_dim, seed):
+    """f16-representable K/V rows for the oracle, generated once per shape."""
+    key = (kv_dim, seed)
+    if key in _KV_CACHE and _KV_CACHE[key][0].shape[0] >= n_pos:
+        k, v = _KV_CACHE[key]
+        return k[:n_pos], v[:n_pos]
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((n_pos, kv_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((n_pos, kv_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+    _KV_CACHE[key] = (k, v)
+    return k, v
+
+
+def cpu_attention_rows(rows, *, Hq, Hkv, hd, n_pos, window=0, scale=None, unit, threads, budget_s,
+                       what):
+    """Time the C oracle's attention (cpu.rs:342-387) on sampled query rows:
+    each row is a one-token call at its position (the same computation as
+    that row of a prefill or decode batch).  rows are visited in the given
+    order until budget_s is spent; unit "GB/s" counts decode bytes (f16 K/V
+    read once, q and out), "TFLOP/s" 4*hd*H per visible pair."""
     import numpy as np
     import oracle
-
-    rng = np.random.default_rng(0)
-    k = rng.standard_normal((CTX, HKV * HD), dtype=np.float32).astype(np.float16).astype(np.float32)
-    v = rng.standard_normal((CTX, HKV * HD), dtype=np.float32).astype(np.float16).astype(np.float32)
-    q = rng.standard_normal((1, H * HD), dtype=np.float32)
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        oracle.attention(q, k, v, n_heads=H, n_kv_heads=HKV, head_dim=HD, base_pos=CTX - 1, n_threads=1)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or calls >= 50:
+    k, v = _cpu_kv(n_pos, Hkv * hd, 11)
+    q = np.random.default_rng(12).standard_normal((1, Hq * hd), dtype=np.float32)
+    done, work, t0 = 0, 0.0, time.perf_counter()
+    for pos in rows:
+        oracle.attention(q, k, v, n_heads=Hq, n_kv_heads=Hkv, head_dim=hd, base_pos=int(pos),
+                         window=window, scale=scale, n_threads=threads)
+        lo = max(0, pos - window + 1) if window else 0
+        n_vis = pos - lo + 1
+        work += (2 * n_vis * Hkv * hd * 2 + Hq * hd * 8) if unit == "GB/s" else 4 * hd * Hq * n_vis
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
             break
-    per = el / calls
-    gbs = decode_bytes([CTX]) / per / 1e9
-    return {"value": gbs, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{calls} decode-attention calls at the headline shape (B=1, ctx {CTX}, "
-                      f"H={H}, Hkv={HKV}, hd={HD}), {per * 1e3:.1f} ms each, C oracle -O2, 1 thread"}
+    el = time.perf_counter() - t0
+    val = work / el / (1e9 if unit == "GB/s" else 1e12)
+    return {"value": val, "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{what}: {done} query rows, {el:.2f} s, C oracle -O2, {threads} thread(s)"}
+
+
+def cpu_delta(T_sample, threads, budget_s):
+    """The C oracle's delta rule (qwen35/cpu.rs:188-246) at the C5 shape over
+    T_sample tokens (threads over v-heads), scaled to C5's bytes per token."""
+    import numpy as np
+    import oracle
+    n_vh, n_kh, sd = 32, 16, 128
+    rng = np.random.default_rng(5)
+    conv = rng.standard_normal((T_sample, 2 * n_kh * sd + n_vh * sd), dtype=np.float32)
+    qk = conv[:, :2 * n_kh * sd].reshape(T_sample, 2 * n_kh, sd)
+    qk /= np.linalg.norm(qk, axis=-1, keepdims=True)
+    al = rng.standard_normal((T_sample, n_vh), dtype=np.float32)
+    be = rng.standard_normal((T_sample, n_vh), dtype=np.float32)
+    S0 = np.zeros((n_vh, sd, sd), np.float32)
+    t0 = time.perf_counter()
+    n_done = 0
+    while True:
+        oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd, n_threads=threads)
+        n_done += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    per_tok = (time.perf_counter() - t0) / (n_done * T_sample)
+    return per_tok
+
+
+def cpu_baselines(budget_s):
+    """One-core and all-core CPU figures per config, keyed like ``extra``."""
+    import numpy as np
+    allc = cpu_cores_all()
+    out = {}
+    _cpu_kv(CTX, HKV * HD, 11)
+    _cpu_kv(CTX, 8 * 256, 11)
+
+    def both(name, fn):
+        t0 = time.perf_counter()
+        out[name] = {"1core": fn(1), "all_cores": fn(allc)}
+        log(f"cpu {name}: 1 core {out[name]['1core']['value']:.4g}, {allc} cores "
+            f"{out[name]['all_cores']['value']:.4g} {out[name]['1core']['unit']} "
+            f"({time.perf_counter() - t0:.1f}s)")
+
+    def spread(S, base, n):  # n positions evenly over the batch
+        return [base + int(x) for x in np.linspace(0, S - 1, n)]
+
+    both("headline", lambda th: cpu_attention_rows([CTX - 1] * 50, Hq=H, Hkv=HKV, hd=HD, n_pos=CTX,
+                                                   unit="GB/s", threads=th, budget_s=budget_s,
+                                                   what="C2 B=1 ctx 32768 decode"))
+    both("decode_c1_ctx512", lambda th: cpu_attention_rows([511] * 20000, Hq=16, Hkv=HKV, hd=HD, n_pos=512,
+                                                           unit="GB/s", threads=th, budget_s=budget_s,
+                                                           what="C1 decode"))
+    for B, seed in ((8, 8), (32, 32)):
+        lens = ragged_lens(B, seed)
+        both(f"decode_b{B}", lambda th, lens=lens, B=B: cpu_attention_rows(
+            [n - 1 for n in lens], Hq=H, Hkv=HKV, hd=HD, n_pos=CTX, unit="GB/s", threads=th,
+            budget_s=budget_s, what=f"C2 B={B} ragged decode, sequences in order"))
+    for S, base in ((512, 0), (2048, 0), (8192, 0), (512, 4096)):
+        name = f"prefill_s{S}" if base == 0 else "prefill_chunk512_on_4k"
+        both(name, lambda th, S=S, base=base: cpu_attention_rows(
+            spread(S, base, 64), Hq=H, Hkv=HKV, hd=HD, n_pos=base + S, unit="TFLOP/s", threads=th,
+            budget_s=budget_s, what=f"C3 prefill S={S} base={base}, rows spread over the batch"))
+    for w, name in ((1024, "gemma_prefill_swa_4k"), (0, "gemma_prefill_global_4k")):
+        both(name, lambda th, w=w: cpu_attention_rows(
+            spread(4096, 0, 64), Hq=16, Hkv=8, hd=256, n_pos=4096, window=w, scale=1 / 16,
+            unit="TFLOP/s", threads=th, budget_s=budget_s, what=f"C4 prefill 4k window={w}"))
+    both("gemma_decode_swa_w1024", lambda th: cpu_attention_rows(
+        [CTX - 1] * 500, Hq=16, Hkv=8, hd=256, n_pos=CTX, window=1024, scale=1 / 16, unit="GB/s",
+        threads=th, budget_s=budget_s, what="C4 SWA decode at 32k"))
+    both("gemma_decode_global", lambda th: cpu_attention_rows(
+        [CTX - 1] * 50, Hq=16, Hkv=8, hd=256, n_pos=CTX, scale=1 / 16, unit="GB/s", threads=th,
+        budget_s=budget_s, what="C4 global decode at 32k"))
+
+    def delta(th, T, name):
+        per_tok = cpu_delta(64, th, budget_s)
+        gbs = delta_bytes(T) / (per_tok * T) / 1e9
+        return {"value": gbs, "unit": "GB/s", "cores": th, "kind": "port",
+                "tokens/s": 1.0 / per_tok,
+                "sample": f"{name}: 64-token runs of the recurrence, {per_tok * 1e3:.3f} ms/token, "
+                          f"C oracle -O2, {th} thread(s)"}
+    both("delta_prefill_T4096_chunked", lambda th: delta(th, 4096, "C5 prefill"))
+    both("delta_decode_1tok", lambda th: delta(th, 1, "C5 decode"))
+    return out
 
 
 def main():
@@ -331,6 +507,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--only", choices=["headline", "all"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=1.0,
+                    help="seconds of CPU timing per config and mode (the headline's 1-core figure "
+                         "gets 10x)")
     ap.add_argument("--extras", default="",
                     help="comma-separated names of the extra configs to run (default: all)")
     ap.add_argument("--pmc-calibration", action="store_true",
@@ -351,8 +530,9 @@ def main():
     lmx.lib()  # fail loudly if the HIP library is missing
 
     log(f"headline: decode B=1 ctx {CTX}, {args.steps} steps, {args.warmup} warmup")
-    ms, gbs, nbytes = bench_decode_headline(lmx, torch, args.steps, args.warmup)
-    log(f"headline: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s")
+    ms, med, nbytes = bench_decode_headline(lmx, torch, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"headline: {ms * 1e3:.2f} us/call (median {med * 1e3:.2f}), {gbs:.1f} GB/s")
 
     extra = {}
     if args.only == "all":
@@ -367,9 +547,11 @@ def main():
             ("prefill_s8192", lambda: bench_prefill(lmx, torch, 8192, steps=5, warmup=1)),
             ("prefill_chunk512_on_4k", lambda: bench_prefill(lmx, torch, 512, base=4096, steps=50, warmup=5)),
             ("gemma_prefill_swa_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,
-                                                           window=1024, scale=1 / 16, steps=5, warmup=1)),
+                                                           window=1024, scale=1 / 16, qk_norm=False,
+                                                           steps=5, warmup=1)),
             ("gemma_prefill_global_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,
-                                                              scale=1 / 16, steps=5, warmup=1)),
+                                                              scale=1 / 16, qk_norm=False, steps=5,
+                                                              warmup=1)),
             ("prologue_prefill_t4096", lambda: bench_prologue(lmx, torch, 4096)),
             ("prologue_decode_t1", lambda: bench_prologue(lmx, torch, 1, steps=50, warmup=5)),
             ("delta_prefill_T4096_chunked", lambda: bench_delta(lmx, torch, 4096, True)),
@@ -378,9 +560,14 @@ def main():
             ("delta_front_T4096", lambda: bench_delta_io(lmx, torch, 4096, "front")),
             ("delta_back_T4096", lambda: bench_delta_io(lmx, torch, 4096, "back")),
             ("matvec_q4k_attn_output_4096", lambda: bench_matvec(lmx, torch, "q4_k", 4096, 4096, 36)),
-            ("matvec_q6k_lm_head_151936", lambda: bench_matvec(lmx, torch, "q6_k", 151936, 4096, 2, steps=20)),
-            ("matvec_q4k_ffn_up_12288", lambda: bench_matvec(lmx, torch, "q4_k", 12288, 4096, 36)),
             ("matvec_q8_0_attn_output_4096", lambda: bench_matvec(lmx, torch, "q8_0", 4096, 4096, 36)),
+            ("matvec_q6k_attn_output_4096", lambda: bench_matvec(lmx, torch, "q6_k", 4096, 4096, 36)),
+            ("gemm_q4k_attn_output_4096_t512", lambda: bench_matvec(lmx, torch, "q4_k", 4096, 4096, 8,
+                                                                    n_tok=512, steps=20)),
+            ("gemm_q6k_attn_output_4096_t512", lambda: bench_matvec(lmx, torch, "q6_k", 4096, 4096, 8,
+                                                                    n_tok=512, steps=20)),
+            ("gemm_q8_0_attn_output_4096_t512", lambda: bench_matvec(lmx, torch, "q8_0", 4096, 4096, 8,
+                                                                     n_tok=512, steps=20)),
             ("kvm_wipe_qwen3_8b_32k", lambda: bench_kvm(lmx, torch, "wipe")),
             ("kvm_batch_tables_b32", lambda: bench_kvm(lmx, torch, "batch")),
         ]:
@@ -402,8 +589,17 @@ def main():
         torch.cuda.synchronize()
         del a, b
 
-    cpu = None if args.skip_cpu else cpu_baseline()
-    if cpu:
+    cpu = None
+    if not args.skip_cpu:
+        cpus = cpu_baselines(args.cpu_budget)
+        for name, v in cpus.items():
+            if name != "headline" and name in extra:
+                extra[name]["cpu"] = v
+        # the headline's one-core figure on a longer sample (about 10 s)
+        cpu = cpu_attention_rows([CTX - 1] * 50, Hq=H, Hkv=HKV, hd=HD, n_pos=CTX, unit="GB/s",
+                                 threads=1, budget_s=10 * args.cpu_budget,
+                                 what="C2 B=1 ctx 32768 decode (the headline shape)")
+        cpu["all_cores"] = cpus["headline"]["all_cores"]
         log(f"cpu baseline: {cpu}")
 
     line = {
@@ -414,6 +610,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "median_ms_per_step": med,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

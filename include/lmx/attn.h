@@ -171,7 +171,8 @@ lmx_status lmx_attn_prologue(const lmx_prologue_desc *d, float *q, const float *
  * batch before attending, so a windowed batch with base_pos+t > window reads
  * slots that later rows of the same batch overwrote; this call refuses that
  * case (LMX_E_RING_HAZARD) unless k_cur/v_cur are given.
- * q_dt: LMX_F32 or LMX_F16.  kv_dt: LMX_F16.
+ * q_dt: LMX_F32 or LMX_F16.  kv_dt: LMX_F16.  out may not overlap q
+ * (LMX_E_SHAPE): workgroups write out while others still read queries.
  * Workspace: lmx_attn_workspace_bytes(p) bytes, zeroed once by
  * lmx_workspace_init; 0 bytes may be asked for (ws may then be NULL).  It
  * holds the split partials of decode, and of prefill when a short batch on a
@@ -395,10 +396,17 @@ lmx_status lmx_kvm_begin(lmx_kvm *m, int32_t seq, const int32_t *tokens, uint32_
  * len += n and the ids join the resident list (session.rs:568, 607-609).
  * tokens == NULL marks rows from an embedding span: the sequence stops being
  * comparable for prefix reuse (session.rs:569-571).  LMX_E_CONTEXT when
- * len + n > n_ctx. */
+ * len + n > n_ctx; LMX_E_RING_HAZARD on a sequence a truncate left stale. */
 lmx_status lmx_kvm_commit(lmx_kvm *m, int32_t seq, const int32_t *tokens, uint32_t n);
 
-/* cache.rs:146-149: drop everything from pos onward (len = min(len, pos)). */
+/* cache.rs:146-149: drop everything from pos onward (len = min(len, pos)).
+ * A ring layer stores position p in slot p % ring, so once positions past
+ * the new end have been written, the slots of some positions the next query
+ * at len must see hold later ones (a ring of w >= 2 slots, positions [0, hw)
+ * written since the last wipe: stale when hw >= len + 2 and hw >= w + 1).
+ * Such a truncate leaves the sequence stale: it is no longer comparable for
+ * prefix reuse (so the next lmx_kvm_begin wipes it), and lmx_kvm_commit and
+ * lmx_kvm_batch return LMX_E_RING_HAZARD for it until it is wiped. */
 lmx_status lmx_kvm_truncate(lmx_kvm *m, int32_t seq, uint32_t pos);
 
 /* cache.rs:138-143: zero the sequence's caches on `stream`, len = 0. */
@@ -413,7 +421,8 @@ lmx_status lmx_kvm_layer_cache(const lmx_kvm *m, int32_t seq, uint32_t layer, vo
 /* Host tables of lmx_attn_decode_batched for layer `layer` over seqs[0, n):
  * k_ptrs/v_ptrs[b] = the sequence's caches, ctx_lens[b] = its len + extra
  * (extra: rows appended for this step but not yet committed, 1 for a decode
- * step), *max_ctx = the largest.  The caller copies the tables to the device. */
+ * step), *max_ctx = the largest.  The caller copies the tables to the device.
+ * LMX_E_RING_HAZARD when a sequence was left stale by lmx_kvm_truncate. */
 lmx_status lmx_kvm_batch(const lmx_kvm *m, uint32_t layer, const int32_t *seqs, uint32_t n,
                          uint32_t extra, const void **k_ptrs, const void **v_ptrs,
                          int32_t *ctx_lens, int32_t *max_ctx);

@@ -309,12 +309,23 @@ class Workspace:
             self.ensure(nbytes)
 
     def ensure(self, nbytes: int, stream=None):
+        """Grow to at least ``nbytes`` for work enqueued on ``stream`` (None:
+        torch's current stream).  torch's caching allocator orders frees and
+        reuse on the current stream only, so on another stream both the new
+        buffer and a replaced one are marked as used there
+        (``record_stream``): neither is handed out again while the stream
+        still has this workspace's kernels queued."""
         torch = _torch()
         if nbytes <= self.nbytes:
             return self
+        side = stream is not None and stream != torch.cuda.current_stream()
+        if side and self.buf is not None:
+            self.buf.record_stream(stream)
         nbytes = (nbytes + 255) // 256 * 256
         self.buf = torch.empty(nbytes + 256, dtype=torch.uint8,
                                device=self.device or torch.device("cuda"))
+        if side:
+            self.buf.record_stream(stream)
         off = (-self.buf.data_ptr()) % 256
         self.base = self.buf.data_ptr() + off
         self.nbytes = nbytes

@@ -271,25 +271,23 @@ lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, con
         return LMX_E_ALIGN;
     if (k_cur && (!aligned(k_cur, 16) || !aligned(v_cur, 16))) return LMX_E_ALIGN;
     const uint32_t hd = p->head_dim;
-    AttnIo io{(int)hd, (int)hd, nullptr};
-    if (x) {
-        const uint32_t qs = x->q_stride ? x->q_stride : hd;
-        const uint32_t gs = x->gate_stride ? x->gate_stride : hd;
-        if (qs < hd || qs % 8 || gs < hd || gs % 4) return LMX_E_SHAPE;
-        if ((uint64_t)p->n_tokens * p->n_heads * qs > INT32_MAX ||
-            (uint64_t)p->n_tokens * p->n_heads * gs > INT32_MAX)
-            return LMX_E_SHAPE;
-        if (x->gate && !aligned(x->gate, 16)) return LMX_E_ALIGN;
-        // out must not overlap what the kernels read after writing it
-        const size_t q_bytes = ((size_t)p->n_tokens * p->n_heads - 1) * qs * (q_dt == LMX_F32 ? 4 : 2) +
-                               (size_t)hd * (q_dt == LMX_F32 ? 4 : 2);
-        const size_t o_bytes = (size_t)p->n_tokens * p->n_heads * hd * 4;
-        if (overlaps(out, o_bytes, q, q_bytes)) return LMX_E_SHAPE;
-        if (x->gate && overlaps(out, o_bytes, x->gate,
-                                (((size_t)p->n_tokens * p->n_heads - 1) * gs + hd) * 4))
-            return LMX_E_SHAPE;
-        io = AttnIo{(int)qs, (int)gs, x->gate};
-    }
+    const uint32_t qs = x && x->q_stride ? x->q_stride : hd;
+    const uint32_t gs = x && x->gate_stride ? x->gate_stride : hd;
+    const float* gate = x ? x->gate : nullptr;
+    if (qs < hd || qs % 8 || gs < hd || gs % 4) return LMX_E_SHAPE;
+    if ((uint64_t)p->n_tokens * p->n_heads * qs > INT32_MAX ||
+        (uint64_t)p->n_tokens * p->n_heads * gs > INT32_MAX)
+        return LMX_E_SHAPE;
+    if (gate && !aligned(gate, 16)) return LMX_E_ALIGN;
+    // out must not overlap what the kernels read after another workgroup
+    // may have written it: the queries and the gate
+    const size_t q_bytes = ((size_t)p->n_tokens * p->n_heads - 1) * qs * (q_dt == LMX_F32 ? 4 : 2) +
+                           (size_t)hd * (q_dt == LMX_F32 ? 4 : 2);
+    const size_t o_bytes = (size_t)p->n_tokens * p->n_heads * hd * 4;
+    if (overlaps(out, o_bytes, q, q_bytes)) return LMX_E_SHAPE;
+    if (gate && overlaps(out, o_bytes, gate, (((size_t)p->n_tokens * p->n_heads - 1) * gs + hd) * 4))
+        return LMX_E_SHAPE;
+    const AttnIo io{(int)qs, (int)gs, gate};
     if (use_split_k(p, q_dt))
         return decode_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
                           (hipStream_t)stream);

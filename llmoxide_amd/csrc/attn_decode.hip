@@ -1,5 +1,7 @@
 // Split-K attention for few query tokens (decode): planning and entry points.
 // The kernels and their design notes are in attn_decode.hpp.
+#include <algorithm>
+
 #include "attn_decode.hpp"
 
 namespace lmx {
@@ -68,6 +70,10 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
     if (P > kMaxP) P = kMaxP;
     if (P < 1) P = 1;
     const long tps = (n_tiles + P - 1) / P;
+    // The workspace is sized for P before empty splits are dropped: that
+    // count grows with the context, the count after dropping does not (12
+    // tiles in 5 splits of 3 use 4 splits, 10 tiles in 5 splits of 2 use 5).
+    pl.P_ws = (int)P;
     P = (n_tiles + tps - 1) / tps;  // drop splits that would be empty
     pl.P = (int)P;
     pl.tps = (int)tps;
@@ -89,11 +95,21 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
         pl.ml_bytes = round_up((size_t)n_q * H * P * 2 * 4, 256);
         pl.o_bytes = round_up((size_t)n_q * H * P * hd * 4, 256);
     }
+    if (pl.P_ws > 1)
+        pl.ws_bytes = round_up((size_t)n_q * H * pl.P_ws * 2 * 4, 256) +
+                      round_up((size_t)n_q * H * pl.P_ws * hd * 4, 256);
     return pl;
 }
 
-
-
+// Workspace for up to n_q query rows whose visible ranges are at most
+// max_vis keys: the largest need over 1..n_q rows, so that a workspace sized
+// for a batch also serves every smaller one (the split count per row falls
+// as rows are added, and n_q * P can dip when it does).
+static size_t decode_ws_upto(int n_q, int H, int Hkv, int hd, int max_vis) {
+    size_t need = 0;
+    for (int n = 1; n <= n_q; ++n) need = std::max(need, plan_decode(n, H, Hkv, hd, max_vis).ws_bytes);
+    return need;
+}
 
 // Longest visible range over the batch's queries (attn.wgsl:52-66 maximized
 // over the tokens; O(t) and t is small on this path).
@@ -114,17 +130,14 @@ int decode_max_vis(const lmx_attn_params* p) {
 }
 
 size_t decode_workspace_bytes(const lmx_attn_params* p) {
-    const DecodePlan pl = plan_decode((int)p->n_tokens, (int)p->n_heads, (int)p->n_kv_heads,
-                                      (int)p->head_dim, decode_max_vis(p));
-    return pl.total();
+    return decode_ws_upto((int)p->n_tokens, (int)p->n_heads, (int)p->n_kv_heads, (int)p->head_dim,
+                          decode_max_vis(p));
 }
 
 size_t decode_batched_workspace_bytes(const lmx_attn_params* p, int n_seq, int max_ctx) {
     int mv = max_ctx;
     if (p->window && (int)p->window < mv) mv = (int)p->window;
-    const DecodePlan pl = plan_decode(n_seq, (int)p->n_heads, (int)p->n_kv_heads,
-                                      (int)p->head_dim, mv);
-    return pl.total();
+    return decode_ws_upto(n_seq, (int)p->n_heads, (int)p->n_kv_heads, (int)p->head_dim, mv);
 }
 
 // Multiply-high constants for p % window over 31-bit p (Granlund-Montgomery:

@@ -644,9 +644,11 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
 
 struct DecodePlan {
     int P, tps, n_hblk, gb, hw;
+    int P_ws;          // splits the workspace is sized for (>= P)
     int n_main, n_yg;
     int n_merge, m_cols, m_parts, m_heads, m_slices;
-    size_t ml_bytes, o_bytes;
+    size_t ml_bytes, o_bytes;  // what this launch uses
+    size_t ws_bytes;           // what the workspace query reports for this shape
     size_t total() const { return ml_bytes + o_bytes; }
 };
 

@@ -6,7 +6,8 @@
 //
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q rows
 //                 held in registers for the whole key loop
-//   online softmax in fp32 (exp2 with scale*log2e folded in), P rounded to f16
+//   online softmax in fp32 (exp2; scale*log2e applied to the fp32 scores of
+//                 an f16 query, folded into an fp32 query), P rounded to f16
 //   O^T += V^T P^T  A = V^T from a transposed LDS tile, B = P straight from the
 //                 S^T accumulators (no shuffle: computing the transpose makes
 //                 each lane own one query column, so softmax is mostly in-lane)
@@ -81,15 +82,23 @@ __device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
 #endif
 template <int HD>
 constexpr int qk_depth() { return HD >= 256 ? LMX_QK_DEPTH_HD256 : 4; }
-template <int HD, int KB, int KPAD>
+//
+// EXACT: Q holds the caller's f16 values and the scores are scaled by
+// c = scale * log2(e) in fp32 after the MFMAs (one FMA per score).  Else c
+// was folded into Q before its one f16 rounding (an fp32 query) and the
+// accumulators start at -mb.  Folding c into a query that is already f16
+// would round it twice: at Gemma's scale 1.0 with unit-RMS heads of 256 the
+// second rounding moves a score by ~2^-12 * c * sqrt(hd) ~ 6e-3 (log2
+// units, one sigma), enough to shift the output past 2e-3.
+template <int HD, int KB, int KPAD, bool EXACT>
 __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16], f32x16 (&s)[KB], float mb,
-                                        int l32, int hh) {
+                                        float c, int l32, int hh) {
     constexpr int KSTEPS = HD / 16, NQ = KSTEPS * KB;
     constexpr int D = qk_depth<HD>() < NQ ? qk_depth<HD>() : NQ;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[kb][i] = -mb;
+        for (int i = 0; i < 16; ++i) s[kb][i] = EXACT ? 0.f : -mb;
     auto rd = [&](int q) {
         const int ks = q / KB, kb = q % KB;
         return *reinterpret_cast<const f16x8*>(&Ks[(kb * 32 + l32) * KPAD + 8 * hh + ks * 16]);
@@ -105,6 +114,12 @@ __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16
         if (q + D < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
     }
+    if constexpr (EXACT) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kb][i] = fmaf(s[kb][i], c, -mb);
+    }
 }
 
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
@@ -115,6 +130,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 
 template <typename QT, int HD>
 __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr bool kExact = sizeof(QT) == 2;  // f16 queries: scale applied in fp32 (qk_tile)
     constexpr int BN = pf_bn<HD>();
     constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
     constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
@@ -158,9 +174,10 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     const int my_lo = qvalid ? vis_lo(qpos, w) : 1;
     const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
 
-    // Q as the B operand: lane holds c * Q[qrow][ks*16 + 8*hh + j], j < 8, with
-    // c = scale * log2(e) folded in before the f16 rounding (one rounding, as
-    // for Q alone), so the S^T accumulators are already exp2 arguments.
+    // Q as the B operand: lane holds Q[qrow][ks*16 + 8*hh + j], j < 8.  An fp32
+    // query has c = scale * log2(e) folded in before its f16 rounding (one
+    // rounding, as for Q alone); an f16 query is used as given and qk_tile
+    // scales its scores.
     f16x8 qf[KSTEPS];
     {
         const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
@@ -182,7 +199,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(x[j] * a.c);
+            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
         }
     }
 
@@ -324,7 +341,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         //      come out already shifted for exp2.
         float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
-        qk_tile<HD, KB, KPAD>(Ks, qf, s, mb, l32, hh);
+        qk_tile<HD, KB, KPAD, kExact>(Ks, qf, s, mb, a.c, l32, hh);
 
         // ---- mask, online softmax.  s[kb][i] is key
         //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
@@ -510,6 +527,7 @@ constexpr int kPpBM = 256;  // query rows per workgroup: 8 waves x 32
 
 template <typename QT, int HD>
 __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) {
+    constexpr bool kExact = sizeof(QT) == 2;  // f16 queries: scale applied in fp32 (qk_tile)
     constexpr int BN = 64;
     constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
     constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
@@ -568,7 +586,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(x[j] * a.c);
+            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
         }
     }
 
@@ -701,7 +719,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     // S^T - mb = K Q^T - mb; mb is the running max once one is set.
     auto qk = [&](const f16* Ks) {
         mb = m_run > -1e29f ? m_run : 0.f;
-        qk_tile<HD, KB, KPAD>(Ks, qf, s, mb, l32, hh);
+        qk_tile<HD, KB, KPAD, kExact>(Ks, qf, s, mb, a.c, l32, hh);
     };
     // s[kb][i] is key kt + 32*kb + 8*(i/4) + 4*hh + i%4 of query qrow.
     auto mask = [&](int kt) {

@@ -34,9 +34,24 @@ struct LayerMap {
 struct Seq {
     bool open = false;
     bool comparable = true;  // the resident ids describe the whole cache
+    bool stale = false;      // a ring slot holds a position past len (after a truncate)
     uint32_t len = 0;
+    uint32_t hw = 0;         // positions [0, hw) were written since the last wipe
     std::vector<int32_t> cached;
 };
+
+// After positions [0, hw) were stored in order into a ring of w slots, does
+// continuing at position pos read a slot that a later position overwrote?
+// The query at pos sees [max(0, pos - w + 1), pos]; slot x % w of a visible
+// x < pos holds x only if no y in (x, hw) with y = x (mod w) was stored, and
+// the first such y is x + w.  Some visible x has x + w < hw exactly when
+// max(pos + 1, w) <= min(hw - 1, pos + w - 1).
+bool ring_stale(uint32_t w, uint32_t hw, uint32_t pos) {
+    if (w < 2 || hw == 0) return false;
+    const uint64_t lo = std::max<uint64_t>((uint64_t)pos + 1, w);
+    const uint64_t hi = std::min<uint64_t>((uint64_t)hw - 1, (uint64_t)pos + w - 1);
+    return lo <= hi;
+}
 
 // Validates d and lays out one sequence slab; false for an invalid description.
 bool plan(const lmx_kvm_desc* d, std::vector<LayerMap>& map, size_t& slab) {
@@ -74,6 +89,7 @@ struct lmx_kvm {
     size_t slab = 0;
     char* arena = nullptr;
     uint32_t n_ctx = 0;
+    std::vector<uint32_t> rings;  // ring sizes of the cache-owning windowed layers
 
     Seq* seq(int32_t s) {
         if (s < 0 || (size_t)s >= seqs.size() || !seqs[s].open) return nullptr;
@@ -94,8 +110,10 @@ struct lmx_kvm {
     lmx_status wipe(int32_t s, lmx_stream st) {
         Seq& q = seqs[s];
         q.len = 0;
+        q.hw = 0;
         q.cached.clear();
         q.comparable = true;
+        q.stale = false;
         return lmx_workspace_init(slab_of(s), slab, st);
     }
 };
@@ -128,6 +146,8 @@ lmx_status lmx_kvm_create(const lmx_kvm_desc* d, void* arena, size_t arena_bytes
             return LMX_E_WORKSPACE;
         }
         m->seqs.resize(d->max_seqs);
+        for (uint32_t i = 0; i < d->n_layers; ++i)
+            if (m->map[i].owner == i && m->map[i].window) m->rings.push_back(m->map[i].window);
         m->arena = static_cast<char*>(arena);
         m->n_ctx = d->n_ctx;
         *out = m;
@@ -194,6 +214,7 @@ lmx_status lmx_kvm_commit(lmx_kvm* m, int32_t seq, const int32_t* tokens, uint32
     if (!m) return LMX_E_NULL;
     Seq* q = m->seq(seq);
     if (!q) return LMX_E_SHAPE;
+    if (q->stale) return LMX_E_RING_HAZARD;
     if ((uint64_t)q->len + n > m->n_ctx) return LMX_E_CONTEXT;
     try {
         if (!tokens) {
@@ -206,6 +227,7 @@ lmx_status lmx_kvm_commit(lmx_kvm* m, int32_t seq, const int32_t* tokens, uint32
         return LMX_E_HOST;
     }
     q->len += n;
+    q->hw = std::max(q->hw, q->len);
     return LMX_OK;
 }
 
@@ -215,6 +237,14 @@ lmx_status lmx_kvm_truncate(lmx_kvm* m, int32_t seq, uint32_t pos) {
     if (!q) return LMX_E_SHAPE;
     q->len = std::min(q->len, pos);  // cache.rs:146-149
     if (q->cached.size() > q->len) q->cached.resize(q->len);
+    // Ring layers have already overwritten slots of positions before the new
+    // end with positions past it: the sequence can only restart from a wipe.
+    for (uint32_t w : m->rings)
+        if (ring_stale(w, q->hw, q->len)) q->stale = true;
+    if (q->stale) {
+        q->comparable = false;
+        q->cached.clear();
+    }
     return LMX_OK;
 }
 
@@ -246,6 +276,7 @@ lmx_status lmx_kvm_batch(const lmx_kvm* m, uint32_t layer, const int32_t* seqs, 
     for (uint32_t b = 0; b < n; ++b) {
         const Seq* q = m->seq(seqs[b]);
         if (!q) return LMX_E_SHAPE;
+        if (q->stale) return LMX_E_RING_HAZARD;
         const uint64_t ctx = (uint64_t)q->len + extra;
         if (ctx == 0) return LMX_E_SHAPE;
         if (ctx > m->n_ctx) return LMX_E_CONTEXT;

@@ -105,6 +105,7 @@ def lib() -> ctypes.CDLL:
         L.orc_attention.argtypes = [P(OrcAttn), f32p, f32p, f32p, f32p, ctypes.c_int, ctypes.c_int]
         L.orc_attention.restype = ctypes.c_int
         L.orc_delta_recur.argtypes = [P(OrcDop)] + [f32p] * 7
+        L.orc_delta_recur_mt.argtypes = [P(OrcDop)] + [f32p] * 7 + [ctypes.c_int]
         L.orc_l2_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
         L.orc_rms_norm_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
         L.orc_rope_neox.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, f32p,
@@ -232,8 +233,11 @@ def attention(q, k, v, *, n_heads, n_kv_heads, head_dim, base_pos, window=0,
     return out
 
 
-def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=None):
-    """Gated delta rule (qwen35/cpu.rs:218-245).  Returns (out, S_new)."""
+def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=None,
+                n_threads=1):
+    """Gated delta rule (qwen35/cpu.rs:218-245).  Returns (out, S_new).
+    ``n_threads`` > 1 splits the independent v-heads over threads; each value
+    is computed the same way."""
     conv = np.ascontiguousarray(conv, np.float32)
     n_tok, conv_dim = conv.shape
     key_dim, d_inner = n_kh * s_dim, n_vh * s_dim
@@ -246,8 +250,8 @@ def delta_recur(conv, alpha, beta, S, *, n_vh, n_kh, s_dim, ssm_a=None, dt_bias=
     out = np.zeros((n_tok, d_inner), np.float32)
     op = OrcDop(n_tok, conv_dim, key_dim, d_inner, s_dim, n_vh, n_kh,
                 np.float32(1.0) / np.sqrt(np.float32(s_dim)))
-    lib().orc_delta_recur(ctypes.byref(op), _f32p(ssm_a), _f32p(dt_bias), _f32p(alpha),
-                          _f32p(beta), _f32p(conv), _f32p(S), _f32p(out))
+    lib().orc_delta_recur_mt(ctypes.byref(op), _f32p(ssm_a), _f32p(dt_bias), _f32p(alpha),
+                             _f32p(beta), _f32p(conv), _f32p(S), _f32p(out), int(n_threads))
     return out, S
 
 

@@ -331,9 +331,9 @@ static float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
  *   S      [n_vh, s_dim (value row j), s_dim (key col)]  updated in place
  *   out    [n_tok, d_inner]
  * The v-head -> k-head map tiles: hk = hv % n_kh (cpu.rs:220). */
-void orc_delta_recur(const orc_dop *op, const float *ssm_a, const float *dt_bias,
-                     const float *alpha, const float *beta, const float *conv,
-                     float *S, float *out) {
+static void orc_delta_heads(const orc_dop *op, const float *ssm_a, const float *dt_bias,
+                            const float *alpha, const float *beta, const float *conv,
+                            float *S, float *out, int64_t hv_begin, int64_t hv_end) {
     const int64_t sd = op->s_dim;
     for (int64_t i = 0; i < op->n_tok; ++i) {
         const float *row_c = conv + i * op->conv_dim;
@@ -341,7 +341,7 @@ void orc_delta_recur(const orc_dop *op, const float *ssm_a, const float *dt_bias
         const float *kn = row_c + op->key_dim;
         const float *vals = row_c + 2 * op->key_dim;
         float *o = out + i * op->d_inner;
-        for (int64_t hv = 0; hv < op->n_vh; ++hv) {
+        for (int64_t hv = hv_begin; hv < hv_end; ++hv) {
             const int64_t hk = (hv % op->n_kh) * sd;
             const float *qh = qn + hk, *kh = kn + hk, *vh = vals + hv * sd;
             const float g = expf(ssm_a[hv] * orc_softplus(alpha[i * op->n_vh + hv] + dt_bias[hv]));
@@ -361,6 +361,50 @@ void orc_delta_recur(const orc_dop *op, const float *ssm_a, const float *dt_bias
             }
         }
     }
+}
+
+void orc_delta_recur(const orc_dop *op, const float *ssm_a, const float *dt_bias,
+                     const float *alpha, const float *beta, const float *conv,
+                     float *S, float *out) {
+    orc_delta_heads(op, ssm_a, dt_bias, alpha, beta, conv, S, out, 0, op->n_vh);
+}
+
+typedef struct {
+    const orc_dop *op;
+    const float *ssm_a, *dt_bias, *alpha, *beta, *conv;
+    float *S, *out;
+    int64_t begin, end;
+} orc_delta_job;
+
+static void *orc_delta_run(void *arg) {
+    const orc_delta_job *j = (const orc_delta_job *)arg;
+    orc_delta_heads(j->op, j->ssm_a, j->dt_bias, j->alpha, j->beta, j->conv, j->S, j->out,
+                    j->begin, j->end);
+    return NULL;
+}
+
+/* The same recurrence with the v-heads split over n_threads pthreads.  The
+ * heads are independent (each owns its S and its output columns), so every
+ * value is computed by the same operations in the same order as above. */
+void orc_delta_recur_mt(const orc_dop *op, const float *ssm_a, const float *dt_bias,
+                        const float *alpha, const float *beta, const float *conv,
+                        float *S, float *out, int n_threads) {
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > (int)op->n_vh) n_threads = (int)op->n_vh;
+    if (n_threads > 256) n_threads = 256;
+    if (n_threads == 1) {
+        orc_delta_heads(op, ssm_a, dt_bias, alpha, beta, conv, S, out, 0, op->n_vh);
+        return;
+    }
+    orc_delta_job jobs[256];
+    pthread_t th[256];
+    for (int t = 0; t < n_threads; ++t) {
+        orc_delta_job j = {op, ssm_a, dt_bias, alpha, beta, conv, S, out,
+                           (int64_t)op->n_vh * t / n_threads, (int64_t)op->n_vh * (t + 1) / n_threads};
+        jobs[t] = j;
+        pthread_create(&th[t], NULL, orc_delta_run, &jobs[t]);
+    }
+    for (int t = 0; t < n_threads; ++t) pthread_join(th[t], NULL);
 }
 
 /* ops.rs:197-203: x / max(||x||, eps), per head of `dim` elements. */

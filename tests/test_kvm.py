@@ -176,3 +176,54 @@ def test_arena_size_and_alignment_are_checked():
     with pytest.raises(lmx.LmxError) as e:
         lmx.KvManager([(0, 8, -1)], n_ctx=16, max_seqs=2, arena=(ARENA + 8, BIG))
     assert e.value.status == lmx.Status.E_ALIGN
+
+
+def ring_reads_stale(w, hw, pos):
+    """Brute force: store positions 0..hw-1 in order into a ring of w slots,
+    then ask whether the query at pos sees a slot holding another position
+    than the one it expects (cache.rs:21-38: slot = p % w, visible
+    [max(0, pos - w + 1), pos]; pos itself is rewritten before it is read)."""
+    ring = [None] * w
+    for p in range(hw):
+        ring[p % w] = p
+    lo = max(0, pos - w + 1)
+    return any(ring[x % w] != x for x in range(lo, pos))
+
+
+def test_truncate_on_a_ring_leaves_the_sequence_stale_exactly_when_slots_were_overwritten():
+    for w in (1, 2, 3, 4, 7):
+        for hw in range(0, 17):
+            for pos in range(0, hw + 1):
+                m = manager([(0, 8, -1), (w, 8, -1)], n_ctx=32, max_seqs=1)
+                s = m.open()
+                m.commit(s, list(range(hw)))
+                m.truncate(s, pos)
+                stale = ring_reads_stale(w, hw, pos)
+                if stale:
+                    assert m.reusable_prefix(s, list(range(hw + 1))) == 0
+                    for call in (lambda: m.batch(0, [s]), lambda: m.commit(s, [1])):
+                        with pytest.raises(lmx.LmxError) as e:
+                            call()
+                        assert e.value.status == lmx.Status.E_RING_HAZARD
+                else:
+                    assert m.batch(1, [s])[2] == [pos + 1], (w, hw, pos)
+                    m.commit(s, [1])
+                    assert m.len(s) == pos + 1
+
+
+def test_truncate_on_linear_layers_keeps_the_prefix_reusable():
+    m = manager([(0, 8, -1), (0, 8, 0)], n_ctx=64, max_seqs=1)
+    s = m.open()
+    m.commit(s, list(range(40)))
+    m.truncate(s, 3)
+    assert m.reusable_prefix(s, [0, 1, 2, 9]) == 3
+    m.commit(s, [9])
+    assert m.len(s) == 4
+
+
+def test_a_ring_wider_than_the_context_never_goes_stale():
+    m = manager([(1024, 8, -1)], n_ctx=100, max_seqs=1)   # ring clamps to 100 slots
+    s = m.open()
+    m.commit(s, list(range(100)))
+    m.truncate(s, 10)
+    assert m.reusable_prefix(s, list(range(11))) == 10

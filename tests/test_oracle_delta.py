@@ -109,3 +109,13 @@ def test_planted_khead_mistake_is_detected():
     swapped[:, 2 * key_dim:] = vh[:, [0, 2, 1, 3]].reshape(T, -1)
     o_bad, _ = oracle.delta_recur(swapped, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
     assert np.max(np.abs(o - o_bad)) > 1e-2
+
+
+def test_threaded_recurrence_is_bit_identical():
+    """Splitting the independent v-heads over threads changes no value."""
+    from tests.helpers import delta_inputs
+    conv, al, be, S0, A, dt = delta_inputs(77, T=23, n_vh=6, n_kh=3, sd=16, s0_scale=0.3)
+    o1, s1 = oracle.delta_recur(conv, al, be, S0, n_vh=6, n_kh=3, s_dim=16, n_threads=1)
+    for n in (2, 4, 6, 9):
+        o2, s2 = oracle.delta_recur(conv, al, be, S0, n_vh=6, n_kh=3, s_dim=16, n_threads=n)
+        assert np.array_equal(o1, o2) and np.array_equal(s1, s2)
