@@ -16,7 +16,8 @@ Timing (every config):
     host enqueues the calls while it runs: the events then time the GPU
     executing the calls back to back, not the 8-10 us ctypes launch of each
     call.  ``ms_per_step`` is the mean over the timed region;
-  * median: per-call events over a second pass of the same calls.
+  * median: the median over 10 blocks of a second pass of the same calls
+    (events between blocks only).
 ``roofline.achieved`` = algorithmic bytes per call / mean time per call.
 
 Other configs (C1, ragged batches, prefill, Gemma shape, delta-net, the f-row
@@ -111,17 +112,20 @@ def time_calls(fns, steps, warmup, torch):
     e1.record(st)
     torch.cuda.synchronize()
     mean = e0.elapsed_time(e1) / steps
-    # median over per-call intervals (a second pass; the events add a little)
-    m = min(steps, 200)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(m + 1)]
-    _sleep_ahead(torch, m)
+    # median: a second pass in blocks of calls, events only between blocks
+    # (an event between every two calls adds ~2 us to short calls)
+    nb = max(1, min(10, steps))
+    per_block = max(1, steps // nb)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(nb + 1)]
+    _sleep_ahead(torch, nb * per_block)
     ev[0].record(st)
-    for i in range(m):
-        fns[i % n]()
-        ev[i + 1].record(st)
+    for b in range(nb):
+        for i in range(per_block):
+            fns[(b * per_block + i) % n]()
+        ev[b + 1].record(st)
     torch.cuda.synchronize()
-    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(m))
-    return mean, per[m // 2]
+    per = sorted(ev[b].elapsed_time(ev[b + 1]) / per_block for b in range(nb))
+    return mean, per[nb // 2]
 
 
 def read_traffic(name):

@@ -190,7 +190,8 @@ def check_exact(out, *, t, H, Hkv, hd, ranges):
             err = np.abs(got[:NBITS] - want).max()
             assert err <= 2e-6, f"token {i} head {h}: [{lo}, {hi}] off by {err:.2e}"
             bits = np.where((kvh >> np.arange(4)) & 1, 1.0, -1.0)
-            assert np.array_equal(got[NBITS:NBITS + 4], bits), f"token {i} head {h}: kv head"
+            # +-n * fl(1/n): +-1 within an ulp or two
+            assert np.abs(got[NBITS:NBITS + 4] - bits).max() <= 2e-6, f"token {i} head {h}: kv head"
             assert np.all(got[NBITS + 4:] == 0.0)
             for (a, b) in ((lo - 1, hi), (lo + 1, hi), (lo, hi - 1), (lo, hi + 1)):
                 if 0 <= a <= b:
