@@ -186,6 +186,28 @@ lmx_status lmx_attn_fwd(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,
                         void *ws, size_t ws_bytes, lmx_stream stream);
 
 /* ------------------------------------------------------------------------
+ * lmx_attn_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the
+ * reference: its attention passes share a scratch buffer the model allocates
+ * at load (qwen35.rs:480).  Same parameters, semantics and results as
+ * lmx_attn_fwd; the split partials go to a library-owned scratch array of
+ * LMX_NOALLOC_SCRATCH_BYTES per GPU (resident from the library's first use
+ * on that GPU until the process ends).  Returns LMX_E_WORKSPACE, enqueuing
+ * nothing, when the call needs more (lmx_attn_workspace_bytes(p) is the
+ * need): a 32k-token decode at Qwen3-8B shape needs about 2 MiB, a
+ * 512-token chunk on a 4k cache about 34 MiB.  No entry point allocates,
+ * and this one takes no workspace either.  Every call on one GPU shares
+ * that GPU's scratch, so calls that overlap on one GPU (concurrent streams,
+ * or threads) race; serialize them on one stream. */
+#define LMX_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+lmx_status lmx_attn_fwd_noalloc(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,
+                                const void *k_cache, const void *v_cache, lmx_dtype kv_dt,
+                                const void *k_cur, const void *v_cur, float *out,
+                                lmx_stream stream);
+
+/* ------------------------------------------------------------------------
  * Attention with Qwen3.5's fused query heads and sigmoid output gate (the
  * epilogue of the attention block).  The CPU reference reads query head h of
  * token i in place at q + (i*n_heads + h)*q_stride (q_stride = 2*head_dim when

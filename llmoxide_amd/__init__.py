@@ -57,6 +57,10 @@ class Status(enum.IntEnum):
 
 F32, F16 = 0, 1
 
+# LMX_NOALLOC_SCRATCH_BYTES (include/lmx/attn.h): the per-GPU scratch of
+# lmx_attn_fwd_noalloc
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
 
 class LmxError(RuntimeError):
     """A call rejected by the library; ``.status`` is the :class:`Status`."""
@@ -211,6 +215,8 @@ SIGNATURES = {
                                     _VP, _SZ, _VP]),
     "lmx_attn_fwd_ext": (ctypes.c_int, [_PA, _PX, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP,
                                         _VP, _VP, _VP, _SZ, _VP]),
+    "lmx_attn_fwd_noalloc": (ctypes.c_int, [_PA, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, _VP, _VP,
+                                            _VP, _VP]),
     "lmx_attn_decode_batched_workspace_bytes": (_SZ, [_PA, _I32, _I32]),
     "lmx_attn_decode_batched": (ctypes.c_int, [_PA, _I32, _I32, _VP, _VP, _VP, _VP, ctypes.c_int,
                                                ctypes.c_int, _VP, _VP, _SZ, _VP]),

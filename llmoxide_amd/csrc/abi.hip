@@ -5,6 +5,7 @@
 // host-side checks (ensure! on batch and context, qwen35.rs:1212-1222;
 // forward.rs:1385-1395) and its error enum (llmoxide/src/error.rs:9-47).
 #include <cmath>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -122,6 +123,33 @@ __global__ void kv_append_kernel(const float* __restrict__ src, f16* __restrict_
         h[3] = (f16)x[3];
         *reinterpret_cast<f16x4*>(cache + (size_t)slot * kv_dim + 4 * c4) = h;
     }
+}
+
+// Scratch of lmx_attn_fwd_noalloc: the split partials of decode and of a
+// key-split prefill, for callers that cannot allocate.  Each GPU the library
+// runs on holds one copy for the life of the process.  In host code the name
+// `scratch` is only a handle: kernels get the device address that
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = (size_t)LMX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// The current device's copy of `scratch`, looked up once per device.
+static lmx_status scratch_of_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LMX_E_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+            return LMX_E_DEVICE;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return LMX_OK;
 }
 
 }  // namespace lmx
@@ -293,6 +321,23 @@ lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, con
                           (hipStream_t)stream);
     return prefill_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
                        (hipStream_t)stream);
+}
+
+lmx_status lmx_attn_fwd_noalloc(const lmx_attn_params* p, const void* q, lmx_dtype q_dt,
+                                const void* k_cache, const void* v_cache, lmx_dtype kv_dt,
+                                const void* k_cur, const void* v_cur, float* out,
+                                lmx_stream stream) {
+    lmx_status s = check_attn_params(p);
+    if (s != LMX_OK) return s;
+    const size_t need = lmx_attn_workspace_bytes(p);
+    if (need > kScratchBytes) return LMX_E_WORKSPACE;
+    void* ws = nullptr;
+    if (need > 0) {
+        s = scratch_of_current_device(&ws);
+        if (s != LMX_OK) return s;
+    }
+    return lmx_attn_fwd_ext(p, nullptr, q, q_dt, k_cache, v_cache, kv_dt, k_cur, v_cur, out, ws,
+                            need > 0 ? kScratchBytes : 0, stream);
 }
 
 size_t lmx_attn_decode_batched_workspace_bytes(const lmx_attn_params* p, int32_t n_seq,

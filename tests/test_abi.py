@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 29
+    assert len(names) == 30
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -331,3 +331,25 @@ def test_batched_workspace_grows_with_the_batch():
             b = L.lmx_attn_decode_batched_workspace_bytes(ctypes.byref(p), B, max_ctx)
             assert b >= prev, (max_ctx, B, b, prev)
             prev = b
+
+
+def test_noalloc_validates_and_refuses_shapes_beyond_its_scratch():
+    """lmx_attn_fwd_noalloc checks like lmx_attn_fwd and refuses, before any
+    device work, a call whose partials exceed LMX_NOALLOC_SCRATCH_BYTES."""
+    L = lmx.lib()
+
+    def call(p, q=FAKE, out=FAKE + (1 << 24)):
+        return L.lmx_attn_fwd_noalloc(ctypes.byref(p), q, lmx.F32, FAKE, FAKE, lmx.F16, None, None,
+                                      out, None)
+    assert call(_params(n_tokens=0)) == lmx.Status.E_SHAPE
+    assert call(_params(head_dim=96)) == lmx.Status.E_UNSUPPORTED
+    limit = 64 << 20
+    # the configured shapes fit: C2 decode at 32k, a C3 512-token chunk on 4k
+    for kw in (dict(n_slots=32768, base_pos=32767), dict(n_tokens=512, n_slots=4608, base_pos=4096)):
+        assert 0 < L.lmx_attn_workspace_bytes(ctypes.byref(_params(**kw))) <= limit
+    # a shape beyond the scratch is refused before anything is enqueued
+    candidates = [_params(n_tokens=t, n_heads=80, n_kv_heads=16, head_dim=hd, n_slots=8192,
+                          base_pos=8192 - t) for (t, hd) in ((1024, 512), (2048, 512), (4096, 256))]
+    big = [p for p in candidates if L.lmx_attn_workspace_bytes(ctypes.byref(p)) > limit]
+    assert big
+    assert call(big[0]) == lmx.Status.E_WORKSPACE
