@@ -79,19 +79,16 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
     pl.tps = (int)tps;
     pl.n_main = (int)(P * units);
     if (P > 1) {
-        // Merge layout: parts (a power of two) so that each thread folds at
-        // most kMergePer partials, float4 columns per item, items per
-        // workgroup to fill its kDecThreads threads.
+        // Merge layout: parts (a power of two <= 64) lanes per float4 column,
+        // so that each folds at most kMergePer partials.
+        static const long parts_env = env_long("LMX_DECODE_MERGE_PARTS", 0);
         int parts = 1;
         while (parts * kMergePer < P) parts <<= 1;
-        int cols = hd / 4;
-        while (cols * parts > kDecThreads) cols >>= 1;
+        if (parts_env >= parts && parts_env <= 64 && (parts_env & (parts_env - 1)) == 0)
+            parts = (int)parts_env;
         pl.m_parts = parts;
-        pl.m_cols = cols;
-        pl.m_heads = kDecThreads / (cols * parts);
-        pl.m_slices = (hd / 4) / cols;
-        const long items = (long)n_q * H * pl.m_slices;
-        pl.n_merge = (int)((items + pl.m_heads - 1) / pl.m_heads);
+        const long cols = (long)n_q * H * (hd / 4);
+        pl.n_merge = (int)((cols * parts + kDecThreads - 1) / kDecThreads);
         pl.ml_bytes = round_up((size_t)n_q * H * P * 2 * 4, 256);
         pl.o_bytes = round_up((size_t)n_q * H * P * hd * 4, 256);
     }
@@ -172,10 +169,7 @@ static lmx_status run(DecodeArgs a, const DecodePlan& pl, int n_q, int hd, lmx_d
     a.n_main = pl.n_main;
     a.n_yg = pl.n_yg;
     a.n_merge = pl.n_merge;
-    a.m_cols = pl.m_cols;
     a.m_parts = pl.m_parts;
-    a.m_heads = pl.m_heads;
-    a.m_slices = pl.m_slices;
     window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
     (void)hipGetLastError();
     lmx_status s;

@@ -40,9 +40,13 @@
 // each split workgroup stores one partial (max, sum, o[hd]) per query head
 // and a second, small kernel merges them: each of its threads folds up to
 // eight partials of one float4 column (all loads issued at once), and the
-// parts of a column are combined in an LDS tree.  The launch boundary
-// orders the partial stores before the merge loads; no counters, so the
-// pair can be replayed from a captured graph as is.
+// parts of a column, adjacent lanes of one wave, are combined by shuffles.
+// The launch boundary orders the partial stores before the merge loads; no
+// counters, so the pair can be replayed from a captured graph as is.  (A
+// single-launch form, where the last split workgroup of a unit merges it,
+// needs a device-scope release and acquire in every workgroup: on gfx950
+// those write back and invalidate the XCD's L2, and the kernel took 67 us
+// instead of 24.)
 #pragma once
 
 #include <climits>
@@ -75,7 +79,7 @@ struct DecodeArgs {
     int P, tps, n_hblk;
     int n_q;                // query rows (tokens, or sequences when batched)
     int n_main, n_yg;       // split workgroups; their (kv group, head block) count
-    int n_merge, m_cols, m_parts, m_heads, m_slices;  // merge workgroup layout
+    int n_merge, m_parts;   // merge workgroups; lanes per merged column
     int max_ctx;            // batched: context lengths are clamped to [1, max_ctx]
     uint32_t w_magic;       // p % window == p - window * ((p * w_magic) >> w_shift)
     int w_shift;
@@ -87,6 +91,9 @@ constexpr int kDecThreads = kWaves * 64;
 constexpr int kMaxP = 512;  // splits per unit
 constexpr int kTile = 16;   // keys per wave tile
 constexpr int kMergePer = 8;            // partials per merge thread
+#ifndef LMX_DEC_DEPTH_128
+#define LMX_DEC_DEPTH_128 2  // K/V tiles in flight per wave at head_dim 128
+#endif
 
 // Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
 // batched: the sequence's last position).
@@ -152,33 +159,31 @@ __device__ __forceinline__ f16x4 ld_stream4(const f16* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
 }
 
-// Merge workgroup blockIdx.x: thread (hl, part, col) folds partials part,
-// part + m_parts, ... (at most kMergePer) of float4 column col of item
-// blockIdx.x * m_heads + hl, where an item is (query row, head, slice of
-// 4 * m_cols dims).  Items whose row had a single split were written by the
-// split kernel and are skipped.
+// Merge: thread (column, part) folds partials part, part + m_parts, ... (at
+// most kMergePer) of one float4 column of one (query row, head), issuing all
+// its loads at once.  The m_parts lanes of a column are adjacent in the wave
+// (m_parts is a power of two <= 64), so they combine by shuffles: no LDS and
+// no barrier.  Rows with a single split were written by the split kernel and
+// are skipped.
 template <int HD, int MODE>
 __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
+    constexpr int C4 = HD / 4;  // float4 columns of a head
     const int tid = threadIdx.x;
-    const int cols = a.m_cols, parts = a.m_parts;
-    const int hl = tid / (cols * parts);
-    const int part = (tid / cols) % parts, col = tid % cols;
-    const int item = blockIdx.x * a.m_heads + hl;
-    const bool have = hl < a.m_heads && item < a.n_q * a.H * a.m_slices;
-    const int slice = item % a.m_slices;
-    const int rest = item / a.m_slices;
-    const int h = rest % a.H, qi = rest / a.H;
-    int p_u = 0;
-    if (have) {
-        int lo, hi;
-        unit_range<MODE>(a, qi, lo, hi);
-        const int n_tiles = (hi - lo + kTile) / kTile;
-        p_u = (n_tiles + a.tps - 1) / a.tps;
-    }
-    const bool merge = have && p_u > 1;
-    const size_t row = (size_t)qi * a.H + h;
-    const int d0 = 4 * (slice * cols + col);
-    float m_run = -INFINITY, l_run = 0.f;
+    const int parts = a.m_parts;
+    const int part = tid & (parts - 1);
+    const long col = (long)blockIdx.x * (kDecThreads / parts) + tid / parts;
+    const bool have = col < (long)a.n_q * a.H * C4;
+    const long cc = have ? col : 0;
+    const size_t row = (size_t)(cc / C4);  // qi * H + h
+    const int d0 = 4 * (int)(cc % C4);
+    const int qi = (int)(row / a.H);
+    int lo, hi;
+    unit_range<MODE>(a, qi, lo, hi);
+    const int n_tiles = (hi - lo + kTile) / kTile;
+    const int p_u = (n_tiles + a.tps - 1) / a.tps;
+    const bool merge = have && p_u > 1;  // the same for every lane of a column
+    // -1e30: a lane without partials keeps weight 0 in the combine below
+    float m_run = -1e30f, l_run = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (merge) {
         const float* po = a.part_o + row * a.P * HD + d0;
@@ -196,44 +201,27 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < kMergePer; ++k) m_run = fmaxf(m_run, m[k]);
-        if (m_run > -INFINITY) {  // else this thread has no partial: exp2(-inf + inf) is NaN
 #pragma unroll
-            for (int k = 0; k < kMergePer; ++k) {
-                const float w = fast_exp2(m[k] - m_run);  // 0 for the unused slots
-                l_run = fmaf(l[k], w, l_run);
-                acc[0] = fmaf(x[k][0], w, acc[0]);
-                acc[1] = fmaf(x[k][1], w, acc[1]);
-                acc[2] = fmaf(x[k][2], w, acc[2]);
-                acc[3] = fmaf(x[k][3], w, acc[3]);
-            }
+        for (int k = 0; k < kMergePer; ++k) {
+            const float w = fast_exp2(m[k] - m_run);  // 0 for the unused slots
+            l_run = fmaf(l[k], w, l_run);
+            acc[0] = fmaf(x[k][0], w, acc[0]);
+            acc[1] = fmaf(x[k][1], w, acc[1]);
+            acc[2] = fmaf(x[k][2], w, acc[2]);
+            acc[3] = fmaf(x[k][3], w, acc[3]);
         }
     }
-    // Tree over the parts of each (item, column): tid and tid + stride*cols.
-    __shared__ float s_m[kDecThreads], s_l[kDecThreads];
-    __shared__ f32x4 s_acc[kDecThreads];
-    s_m[tid] = m_run;
-    s_l[tid] = l_run;
-    s_acc[tid] = acc;
-    for (int stride = parts / 2; stride >= 1; stride >>= 1) {
-        __syncthreads();
-        if (part < stride) {
-            const int o = tid + stride * cols;
-            const float m2 = s_m[o];
-            const float mn = fmaxf(m_run, m2);
-            if (mn > -INFINITY) {
-                const float c0 = fast_exp2(m_run - mn), c1 = fast_exp2(m2 - mn);
-                const f32x4 y = s_acc[o];
-                l_run = l_run * c0 + s_l[o] * c1;
-                acc[0] = acc[0] * c0 + y[0] * c1;
-                acc[1] = acc[1] * c0 + y[1] * c1;
-                acc[2] = acc[2] * c0 + y[2] * c1;
-                acc[3] = acc[3] * c0 + y[3] * c1;
-                m_run = mn;
-            }
-            s_m[tid] = m_run;
-            s_l[tid] = l_run;
-            s_acc[tid] = acc;
-        }
+    for (int off = 1; off < parts; off <<= 1) {
+        const float m2 = shfl_xor(m_run, off), l2 = shfl_xor(l_run, off);
+        f32x4 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = shfl_xor(acc[j], off);
+        const float mn = fmaxf(m_run, m2);
+        const float c0 = fast_exp2(m_run - mn), c1 = fast_exp2(m2 - mn);
+        l_run = l_run * c0 + l2 * c1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = acc[j] * c0 + y[j] * c1;
+        m_run = mn;
     }
     if (merge && part == 0) {
         const float inv = 1.f / l_run;
@@ -254,7 +242,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     // Tiles in flight per wave (a 16-key tile is 16 K + 16 V registers per
     // lane at hd 128, 8 + 8 at hd 64).  At hd 128 two measured best: with
     // one wave per SIMD, deeper buffers (3, 4, 6) only lengthen the start.
-    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : 2);
+    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : LMX_DEC_DEPTH_128);
     static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
     static_assert(VR * VW == DPL, "V lane layout");
     static_assert(kWaves % HW == 0, "waves per head");
@@ -646,7 +634,7 @@ struct DecodePlan {
     int P, tps, n_hblk, gb, hw;
     int P_ws;          // splits the workspace is sized for (>= P)
     int n_main, n_yg;
-    int n_merge, m_cols, m_parts, m_heads, m_slices;
+    int n_merge, m_parts;
     size_t ml_bytes, o_bytes;  // what this launch uses
     size_t ws_bytes;           // what the workspace query reports for this shape
     size_t total() const { return ml_bytes + o_bytes; }
