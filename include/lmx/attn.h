@@ -340,7 +340,14 @@ lmx_status lmx_deltanet_back(const lmx_delta_back_desc *d, float *o, const float
  *      30 BF16; 16-byte aligned
  *   x  [n_tok, in_dim] f32, y [n_tok, rows] f32, 16-byte aligned, disjoint
  * in_dim: a multiple of 256 (Q4_K, Q6_K) or 64 (the others), at most 16384.
- * Tokens go four per launch; each launch reads W once. */
+ * Below 16 tokens (and for the dense types) tokens go four per launch, each
+ * launch reading W once.  From 16 tokens (the reference's GEMM_MIN_TOKENS,
+ * crates/gpu/src/lib.rs:1083; its GEMM is gemm_q6k, gemm.wgsl:93-95) a Q4_K,
+ * Q6_K or Q8_0 matrix with in_dim a multiple of 128 goes through one
+ * matrix-core GEMM launch that reads W once; it computes each block's
+ * integer dot products exactly and applies the block scales in fp32, and
+ * needs |x| < 65504 (the f16 range; attention outputs over an f16 V cache
+ * always are). */
 typedef struct {
     uint32_t type;
     uint32_t rows;

@@ -1,0 +1,382 @@
+// Quantized GEMM on gfx950 matrix cores: Y[t][r] = sum_k W[r][k] X[t][k] for
+// a batch of tokens (prefill) and a weight matrix in ggml's on-disk block
+// formats Q4_K, Q6_K or Q8_0, read once per launch.
+//
+// Replaces the reference's prefill GEMM (gemm_q6k in gemm.wgsl:93-95 and
+// gemm_q6k.metal:50, chosen from 16 tokens: crates/gpu/src/lib.rs:1039-1046,
+// 1083) and computes what its CPU reference dot_row computes
+// (crates/gguf/src/quant.rs:187-271), to fp32 accuracy:
+//
+//   Every block format is  w = s_g * q + o_g  over groups g of 16 or 32
+//   consecutive weights, q a small integer:
+//     Q4_K  q in [0, 15],     s = d * sc_g, o = -dmin * m_g  (groups of 32)
+//     Q6_K  q in [-32, 31],   s = d * sc_g, o = 0            (groups of 16)
+//     Q8_0  q in [-128, 127], s = d,        o = 0            (groups of 32)
+//   so   y = sum_g  s_g * (sum_{k in g} q_k x_k)  +  o_g * (sum_{k in g} x_k),
+//   the order dot_row itself uses for Q4_K (its s1 and x1 per sub-block).
+//   The integers q are exact in f16; x is split into f16 x_hi + x_lo
+//   (|x - x_hi - x_lo| <= 2^-22 |x|), so each group's integer sum is two
+//   v_mfma_f32_32x32x16_f16 products accumulated in fp32, and the group's
+//   scale and offset are applied in fp32 (the x sums come from the fp32 x).
+//   |x| must stay below 65504, the f16 range (attention outputs over an f16
+//   V cache always do).
+//
+// Tiles.  A workgroup of four waves owns 64 tokens x 128 weight rows; wave
+// (wm, wn) owns tokens 32 wm .. + 31 and rows 64 wn .. + 63: two 32 x 32
+// MFMA tiles, x as the A operand and q as B, so each lane of a result tile
+// holds one weight row and 16 tokens, and a group's scale is one value per
+// lane.  K goes through LDS 128 weights at a time (half a K-quant
+// super-block, four Q8_0 blocks): x as swizzled f16 hi / lo rows, W decoded
+// to f16 integers with each row's group scales, and the (token, group) x
+// sums.  The next chunk's raw x and W bytes are loaded into registers while
+// the current chunk is multiplied.
+#include "common.hpp"
+
+namespace lmx {
+
+enum GType { kGQ8_0 = 8, kGQ4K = 12, kGQ6K = 14 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGM = 64;        // tokens per workgroup
+constexpr int kGN = 128;       // weight rows per workgroup
+constexpr int kGK = 128;       // weights per LDS chunk
+constexpr int kGThreads = 256;
+#ifndef LMX_QGEMM_OCC
+#define LMX_QGEMM_OCC 2  // workgroups per CU the register budget is sized for
+#endif
+
+template <int TY>
+struct GTraits;
+template <> struct GTraits<kGQ4K> { static constexpr int gs = 32, words = 12; };
+template <> struct GTraits<kGQ6K> { static constexpr int gs = 16, words = 15; };
+template <> struct GTraits<kGQ8_0> { static constexpr int gs = 32, words = 18; };
+
+struct GemmArgs {
+    const uint8_t* w;
+    const float* x;
+    float* y;
+    int rows, in_dim, n_tok;
+    size_t row_bytes;
+};
+
+// Swizzled offset (in halfs) of 8-half chunk c of LDS row r: the chunk index
+// is XORed with the row, so the rows an MFMA operand read touches spread
+// over the banks.
+__device__ __forceinline__ int sw(int r, int c) { return r * kGK + ((c ^ (r & 15)) << 3); }
+
+// Eight bytes at a 2-byte aligned address as two dwords: the covering
+// aligned dwords, funnel-shifted.  A shifted read also touches the 2 bytes
+// after the range; every range below ends at least 2 bytes before its block.
+__device__ __forceinline__ void ld8_a2(const uint8_t* p, uint32_t* o) {
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t* b = reinterpret_cast<const uint32_t*>(p - sh);
+    const uint32_t r0 = b[0], r1 = b[1], r2 = sh ? b[2] : 0u;
+    o[0] = __builtin_amdgcn_alignbyte(r1, r0, sh);
+    o[1] = __builtin_amdgcn_alignbyte(r2, r1, sh);
+}
+
+__device__ __forceinline__ float half_bits(uint32_t h) {
+    return (float)__builtin_bit_cast(f16, (uint16_t)(h & 0xFFFF));
+}
+__device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xFF; }
+
+// Raw W bytes of one chunk held by thread (row, part); two threads per row.
+//  Q4_K: chunk = half hf of a super-block; part p takes pair 2 hf + p:
+//        words 0-3 the block header (d, dmin, 12 scale bytes), 4-11 the
+//        pair's 32 quant bytes (sub-blocks 2 (2 hf + p) and + 1).
+//  Q6_K: chunk = half h; part p takes l in [16 p, 16 p + 16) of every
+//        32-wide quarter: words 0-3 ql[16 p ..], 4-7 ql[32 + 16 p ..],
+//        8-11 qh[16 p ..] (of the half), 12-13 the half's 8 scales, 14 d.
+//  Q8_0: chunk = four blocks; part p takes blocks 2 p, 2 p + 1 (68 bytes,
+//        as 17 words from a 2-byte aligned start; word 17 unused).
+template <int TY>
+__device__ __forceinline__ void load_w(const uint8_t* row, int k0, int part, uint32_t* rw) {
+    if constexpr (TY == kGQ4K) {
+        const uint8_t* blk = row + (size_t)(k0 >> 8) * 144;
+        const int hf = (k0 >> 7) & 1;
+        const u32x4 h4 = *reinterpret_cast<const u32x4*>(blk);
+        const u32x4 q0 = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * (2 * hf + part));
+        const u32x4 q1 = *reinterpret_cast<const u32x4*>(blk + 32 + 32 * (2 * hf + part));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            rw[i] = h4[i];
+            rw[4 + i] = q0[i];
+            rw[8 + i] = q1[i];
+        }
+    } else if constexpr (TY == kGQ6K) {
+        const uint8_t* blk = row + (size_t)(k0 >> 8) * 210;
+        const int h = (k0 >> 7) & 1;
+        const uint8_t* ql = blk + 64 * h + 16 * part;
+        const uint8_t* qh = blk + 128 + 32 * h + 16 * part;
+        ld8_a2(ql, rw + 0);
+        ld8_a2(ql + 8, rw + 2);
+        ld8_a2(ql + 32, rw + 4);
+        ld8_a2(ql + 40, rw + 6);
+        ld8_a2(qh, rw + 8);
+        ld8_a2(qh + 8, rw + 10);
+        ld8_a2(blk + 192 + 8 * h, rw + 12);
+        rw[14] = *reinterpret_cast<const uint16_t*>(blk + 208);
+    } else {
+        const uint8_t* blk = row + (size_t)((k0 >> 5) + 2 * part) * 34;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ld8_a2(blk + 8 * i, rw + 2 * i);
+        // the last 4 bytes (block 2p+1's final quants) as two 2-byte loads
+        rw[16] = (uint32_t)reinterpret_cast<const uint16_t*>(blk + 64)[0] |
+                 ((uint32_t)reinterpret_cast<const uint16_t*>(blk + 66)[0] << 16);
+        rw[17] = 0u;
+    }
+}
+
+// Eight small integers as f16 into 8-half chunk c of LDS row r.
+__device__ __forceinline__ void put8(f16* q_s, int r, int c, const int (&v)[8]) {
+    f16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (f16)(float)v[j];
+    *reinterpret_cast<f16x8*>(&q_s[sw(r, c)]) = h;
+}
+
+// Decode thread (row r, part)'s raw bytes into q_s (f16 integers) and its
+// groups' (scale, offset) into so_s.
+template <int TY>
+__device__ __forceinline__ void stash_w(const uint32_t* rw, int k0, int r, int part, bool live, f16* q_s,
+                                        f32x2* so_s) {
+    constexpr int NG = kGK / GTraits<TY>::gs;
+    if constexpr (TY == kGQ4K) {
+        // pair p = 2 hf + part: weights 64 part + e; e < 32 low nibble of
+        // quant byte e, else high nibble of byte e - 32 (quant.rs:54-128)
+        const uint32_t* q = rw + 4;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t b = byte_of(q, 8 * (cc & 3) + j);
+                v[j] = cc < 4 ? (int)(b & 0xF) : (int)(b >> 4);
+            }
+            put8(q_s, r, 8 * part + cc, v);
+        }
+        // sub-blocks j = 2 (2 hf + part) + {0, 1}: scale and min, quant.rs:33-47
+        const int hf = (k0 >> 7) & 1;
+        const float d = half_bits(rw[0]), dmin = half_bits(rw[0] >> 16);
+        const uint32_t* s = rw + 1;  // the 12 scale bytes
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int j = 2 * (2 * hf + part) + t;
+            uint32_t sc, m;
+            if (j < 4) {
+                sc = byte_of(s, j) & 63;
+                m = byte_of(s, j + 4) & 63;
+            } else {
+                sc = (byte_of(s, j + 4) & 0xF) | ((byte_of(s, j - 4) >> 6) << 4);
+                m = (byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4);
+            }
+            so_s[r * NG + 2 * part + t] =
+                live ? f32x2{d * (float)sc, -(dmin * (float)m)} : f32x2{0.f, 0.f};
+        }
+    } else if constexpr (TY == kGQ6K) {
+        // weight 32 k + l of the half: low / high nibble (k >> 1) of
+        // ql[l + 32 (k & 1)], with bits 2k, 2k + 1 of qh[l] on top, minus 32
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int c2 = 0; c2 < 2; ++c2) {
+                int v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int l = 8 * c2 + j;  // l - 16 part
+                    const uint32_t lb = byte_of(rw + 4 * (k & 1), l);
+                    const uint32_t hb = byte_of(rw + 8, l);
+                    v[j] = (int)(((lb >> (4 * (k >> 1))) & 0xF) | (((hb >> (2 * k)) & 3) << 4)) - 32;
+                }
+                put8(q_s, r, 4 * k + 2 * part + c2, v);
+            }
+        }
+        const float d = half_bits(rw[14]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int g = 2 * k + part;
+            const float sc = (float)(int8_t)byte_of(rw + 12, g);
+            so_s[r * NG + g] = live ? f32x2{d * sc, 0.f} : f32x2{0.f, 0.f};
+        }
+    } else {
+        // block b = 2 part + bi: d at bytes 34 bi, quants at 34 bi + 2
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            const int base = 34 * bi;
+            const float d = half_bits(byte_of(rw, base) | (byte_of(rw, base + 1) << 8));
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                int v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = (int)(int8_t)byte_of(rw, base + 2 + 8 * cc + j);
+                put8(q_s, r, 4 * (2 * part + bi) + cc, v);
+            }
+            so_s[r * NG + 2 * part + bi] = live ? f32x2{d, 0.f} : f32x2{0.f, 0.f};
+        }
+    }
+}
+
+template <int TY>
+__global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArgs a) {
+    constexpr int GS = GTraits<TY>::gs;
+    constexpr int NG = kGK / GS;          // groups per chunk
+    constexpr int KPG = GS / 16;          // MFMA k-steps per group
+    constexpr bool OFFSET = TY == kGQ4K;  // groups carry an offset (Q4_K's min)
+    constexpr int WW = GTraits<TY>::words;
+    __shared__ __attribute__((aligned(16))) f16 xh_s[kGM * kGK];
+    __shared__ __attribute__((aligned(16))) f16 xl_s[kGM * kGK];
+    __shared__ __attribute__((aligned(16))) f16 q_s[kGN * kGK];
+    __shared__ __attribute__((aligned(16))) f32x2 so_s[kGN * NG];        // (s, o) per row, group
+    __shared__ __attribute__((aligned(16))) float xs_s[OFFSET ? NG * kGM : 4];  // x sums per group, token
+
+    const int n_tb = (a.n_tok + kGM - 1) / kGM;
+    const int tb = blockIdx.x % n_tb, rb = blockIdx.x / n_tb;
+    const int t0 = tb * kGM, r0 = rb * kGN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    // ---- register prefetch of one chunk
+    // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
+    // consecutive threads read one token's 512 contiguous bytes.
+    f32x4 rx[8];
+    uint32_t rw[WW];
+    const int w_row = tid >> 1, w_part = tid & 1;
+    const bool w_live = r0 + w_row < a.rows;
+    const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = tid + kGThreads * u, tok = i >> 5, k4 = i & 31;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (t0 + tok < a.n_tok)
+                v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
+            rx[u] = v;
+        }
+        load_w<TY>(wrow, k0, w_part, rw);
+    };
+    auto stash_chunk = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = tid + kGThreads * u, tok = i >> 5, k4 = i & 31;
+            f16x4 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                hi[j] = (f16)rx[u][j];
+                lo[j] = (f16)(rx[u][j] - (float)hi[j]);
+            }
+            const int off = sw(tok, k4 >> 1) + 4 * (k4 & 1);
+            *reinterpret_cast<f16x4*>(&xh_s[off]) = hi;
+            *reinterpret_cast<f16x4*>(&xl_s[off]) = lo;
+            if constexpr (OFFSET) {
+                // the group's x sum: eight consecutive lanes hold its 32 floats
+                float sx = (rx[u][0] + rx[u][1]) + (rx[u][2] + rx[u][3]);
+                sx += shfl_xor(sx, 1);
+                sx += shfl_xor(sx, 2);
+                sx += shfl_xor(sx, 4);
+                if ((k4 & 7) == 0) xs_s[(k4 >> 3) * kGM + tok] = sx;
+            }
+        }
+        stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s, so_s);
+    };
+
+    f32x16 y[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[n][j] = 0.f;
+
+    const int n_chunks = a.in_dim / kGK;
+    load_chunk(0);
+    for (int ch = 0; ch < n_chunks; ++ch) {
+        __syncthreads();  // the previous chunk's operand reads are done
+        stash_chunk(ch * kGK);
+        __syncthreads();
+        if (ch + 1 < n_chunks) load_chunk((ch + 1) * kGK);  // in flight during the MFMAs
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            f32x16 acc[2];
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[n][j] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < KPG; ++kk) {
+                const int c = 2 * (g * KPG + kk) + hh;
+                const int xr = 32 * wm + l32;
+                const f16x8 ah = *reinterpret_cast<const f16x8*>(&xh_s[sw(xr, c)]);
+                const f16x8 al = *reinterpret_cast<const f16x8*>(&xl_s[sw(xr, c)]);
+#pragma unroll
+                for (int n = 0; n < 2; ++n) {
+                    const f16x8 b = *reinterpret_cast<const f16x8*>(&q_s[sw(64 * wn + 32 * n + l32, c)]);
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, acc[n], 0, 0, 0);
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, acc[n], 0, 0, 0);
+                }
+            }
+            // tokens of register j: 8 (j / 4) + 4 hh + j % 4 of the wave's 32
+            f32x4 xs[4];
+            if constexpr (OFFSET) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    xs[q4] = *reinterpret_cast<const f32x4*>(&xs_s[g * kGM + 32 * wm + 8 * q4 + 4 * hh]);
+            }
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const f32x2 so = so_s[(64 * wn + 32 * n + l32) * NG + g];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    float v = fmaf(so[0], acc[n][j], y[n][j]);
+                    if constexpr (OFFSET) v = fmaf(so[1], xs[j >> 2][j & 3], v);
+                    y[n][j] = v;
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        const int r = r0 + 64 * wn + 32 * n + l32;
+        if (r >= a.rows) continue;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int t = t0 + 32 * wm + 8 * (j >> 2) + 4 * hh + (j & 3);
+            if (t < a.n_tok) a.y[(size_t)t * a.rows + r] = y[n][j];
+        }
+    }
+}
+
+// y [n_tok, rows] = W x: one launch, W read once from HBM (each of the
+// ceil(n_tok / 64) token blocks of a row block reads it from L2 or the
+// last-level cache after the first).
+lmx_status qgemm(const lmx_qmv_desc* d, const void* w, const float* x, float* y, hipStream_t st) {
+    size_t bb = 0, be = 0;
+    switch (d->type) {
+        case kGQ4K: bb = 144; be = 256; break;
+        case kGQ6K: bb = 210; be = 256; break;
+        case kGQ8_0: bb = 34; be = 32; break;
+        default: return LMX_E_UNSUPPORTED;
+    }
+    if (d->in_dim % kGK || d->in_dim % be) return LMX_E_SHAPE;
+    GemmArgs a{};
+    a.w = static_cast<const uint8_t*>(w);
+    a.x = x;
+    a.y = y;
+    a.rows = (int)d->rows;
+    a.in_dim = (int)d->in_dim;
+    a.n_tok = (int)d->n_tok;
+    a.row_bytes = (size_t)d->in_dim / be * bb;
+    const long n_tb = ((long)d->n_tok + kGM - 1) / kGM, n_rb = ((long)d->rows + kGN - 1) / kGN;
+    if (n_tb * n_rb > INT32_MAX) return LMX_E_SHAPE;
+    const dim3 grid((unsigned)(n_tb * n_rb));
+    (void)hipGetLastError();
+    switch (d->type) {
+        case kGQ4K: hipLaunchKernelGGL(qgemm_kernel<kGQ4K>, grid, dim3(kGThreads), 0, st, a); break;
+        case kGQ6K: hipLaunchKernelGGL(qgemm_kernel<kGQ6K>, grid, dim3(kGThreads), 0, st, a); break;
+        default: hipLaunchKernelGGL(qgemm_kernel<kGQ8_0>, grid, dim3(kGThreads), 0, st, a); break;
+    }
+    LMX_CHECK_LAUNCH();
+    return LMX_OK;
+}
+
+}  // namespace lmx

@@ -510,8 +510,19 @@ static lmx_status launch_type(const QmvArgs& a, int T, hipStream_t st) {
     return LMX_OK;
 }
 
-// Host side: tokens go in tiles of up to kQmvMaxTok (each tile re-reads W).
+// qgemm.hip: the matrix-core GEMM for batches of tokens
+lmx_status qgemm(const lmx_qmv_desc* d, const void* w, const float* x, float* y, hipStream_t st);
+
+// From this many tokens the GEMM takes the k-quant formats (the reference's
+// GEMM_MIN_TOKENS, crates/gpu/src/lib.rs:1083): one launch reads W once.
+constexpr uint32_t kGemmMinTokens = 16;
+
+// Host side: tokens go in tiles of up to kQmvMaxTok (each tile re-reads W),
+// or to the GEMM.
 lmx_status qmatvec(const lmx_qmv_desc* d, const void* w, const float* x, float* y, hipStream_t st) {
+    if (d->n_tok >= kGemmMinTokens && d->in_dim % 128 == 0 &&
+        (d->type == kQ4K || d->type == kQ6K || d->type == kQ8_0))
+        return qgemm(d, w, x, y, st);
     int unit = 0;
     size_t bb = 0, be = 0;
     switch (d->type) {

@@ -69,3 +69,55 @@ def test_partial_and_multiple_chunks(name, rows, in_dim, n_tok):
     # (three full chunks and a 4-unit one); odd Q6_K blocks per row put the
     # chunks' windows at every 2-byte offset mod 16.
     run(name, rows, in_dim, n_tok, seed=11 + rows + n_tok)
+
+
+# ---- the matrix-core GEMM (n_tok >= 16, Q4_K / Q6_K / Q8_0): same bar --
+GEMM_TYPES = ["q4_k", "q6_k", "q8_0"]
+
+
+def run_rows(name, rows, in_dim, n_tok, seed, check_rows):
+    """GEMM over the whole matrix, oracle on the listed rows only."""
+    say(f"gemm {name} rows={rows} in_dim={in_dim} n_tok={n_tok} checked rows={len(check_rows)}")
+    ty = oracle.QTYPES[name]
+    w = oracle.quant_weights(ty, rows, in_dim, seed)
+    x = oracle.normal(seed + 50, (n_tok, in_dim))
+    y = lmx.matvec(torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(), qtype=name, rows=rows,
+                   in_dim=in_dim)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    rb = oracle.row_bytes(ty, in_dim)
+    sub = np.ascontiguousarray(w.reshape(rows, rb)[check_rows])
+    ref = oracle.matvec(ty, sub, len(check_rows), in_dim, x)
+    err = np.abs(got[:, check_rows] - ref).max()
+    assert err <= 3e-5 * np.abs(ref).max(), f"{name}: max err {err} vs max |ref| {np.abs(ref).max()}"
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("name", GEMM_TYPES)
+@pytest.mark.parametrize("n_tok", [16, 64])
+def test_gemm_attn_output_shape(name, n_tok):
+    # Qwen3-8B attn_output 4096 x 4096 at the GEMM threshold and one token block
+    run(name, 4096, 4096, n_tok, seed=20 + n_tok)
+
+
+@pytest.mark.parametrize("name", GEMM_TYPES)
+def test_gemm_prefill_chunk_512(name):
+    # the benched shape: a 512-token chunk through attn_output; every token,
+    # rows from the first, a middle and the last row block
+    rows = list(range(0, 128)) + list(range(2000, 2050)) + list(range(4096 - 130, 4096))
+    run_rows(name, 4096, 4096, 512, seed=31, check_rows=rows)
+
+
+@pytest.mark.parametrize("name,in_dim", [("q4_k", 512), ("q6_k", 768), ("q8_0", 640)])
+@pytest.mark.parametrize("rows,n_tok", [(200, 33), (37, 16), (130, 65)])
+def test_gemm_ragged_edges(name, in_dim, rows, n_tok):
+    # rows and tokens off the 128 x 64 workgroup tile; Q6_K with 3 blocks a
+    # row puts odd rows 2 bytes off a dword; Q8_0 with 20 blocks a row
+    run(name, rows, in_dim, n_tok, seed=40 + rows + n_tok)
+
+
+@pytest.mark.parametrize("name", GEMM_TYPES)
+def test_matvec_and_gemm_agree_across_the_threshold(name):
+    # 15 tokens take the matvec tiles, 16 the GEMM: both match the oracle
+    for n_tok in (15, 16):
+        run(name, 256, 1024, n_tok, seed=60)
