@@ -58,6 +58,13 @@ constexpr int kPfCus = 256;  // compute units of the target (MI355X)
 // the next tile and the o accumulators share one register file).
 template <int HD>
 constexpr int pf_bn() { return HD >= 256 ? 32 : 64; }
+// Output dim slices: at head_dim 512 a wave cannot hold Q and a 32 x 512
+// fp32 output block in registers, so two workgroups share a (head, query
+// tile): each forms the whole S = Q K^T (the same scores and softmax in
+// both) and accumulates P V for its half of the dims, staging only that half
+// of V (1.5x the MFMA work of one pass, the register budget of head_dim 256).
+template <int HD>
+constexpr int pf_dslices() { return HD >= 512 ? 2 : 1; }
 constexpr float kRescaleSlack = 8.f;  // log2 units a running max may lag by
 
 // attn.wgsl:52-66
@@ -76,12 +83,13 @@ __device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
 // (k-step, block) order alternates the KB accumulator chains.  Depth 4 at
 // head_dim <= 128 (6 spills in the 128-row kernel), QK_DEPTH_HD256 at 256,
 // where one wave per SIMD has the registers (measured: depth 4 +2-3% at
-// S = 8192, +7% on Gemma hd 256 global 4k; depth 6 a further +2-3% there).
+// S = 8192, +7% on Gemma hd 256 global 4k; depth 6 a further +2-3% there),
+// and 2 at head_dim 512, whose Q alone takes 128 registers.
 #ifndef LMX_QK_DEPTH_HD256
 #define LMX_QK_DEPTH_HD256 8
 #endif
 template <int HD>
-constexpr int qk_depth() { return HD >= 256 ? LMX_QK_DEPTH_HD256 : 4; }
+constexpr int qk_depth() { return HD >= 512 ? 2 : (HD >= 256 ? LMX_QK_DEPTH_HD256 : 4); }
 //
 // EXACT: Q holds the caller's f16 values and the scores are scaled by
 // c = scale * log2(e) in fp32 after the MFMAs (one FMA per score).  Else c
@@ -132,33 +140,36 @@ template <typename QT, int HD>
 __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(PrefillArgs a) {
     constexpr bool kExact = sizeof(QT) == 2;  // f16 queries: scale applied in fp32 (qk_tile)
     constexpr int BN = pf_bn<HD>();
+    constexpr int DS = pf_dslices<HD>();  // output dim slices, one per workgroup
+    constexpr int HDV = HD / DS;     // V / output dims of this workgroup
     constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
     constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
     constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
-    constexpr int NB = HD / 32;      // 32-dim output blocks
+    constexpr int NB = HDV / 32;     // 32-dim output blocks
     constexpr int KPAD = HD + 8;     // K_s row stride (halfs)
     constexpr int VPAD = BN + 4;     // Vt_s row stride (halfs), 8-byte aligned rows
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
-    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HDV * VPAD];
 
     // ---- which (head, query tile, key split) this workgroup owns
     const int nblk = gridDim.x;
     const int logical = xcd_remap(blockIdx.x, nblk);
     const int n_split = a.n_split;
-    const int per_kvh = a.n_qtiles * a.G * n_split;
+    const int per_kvh = a.n_qtiles * a.G * n_split * DS;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
     // Query tiles heaviest first (causal work grows with qt).  When the whole
     // grid is resident at once (two workgroups per CU), the second half is
     // walked lightest first, so the two workgroups a CU receives pair a heavy
     // tile with a light one instead of two of nearly the same weight.
-    const int pos = rem / (a.G * n_split);
+    const int pos = rem / (a.G * n_split * DS);
     const int half = (a.n_qtiles + 1) / 2;
     const bool fold = HD <= 128 && nblk <= 2 * kPfCus;
     const int qt = (fold && pos >= half) ? pos - half : a.n_qtiles - 1 - pos;
-    const int rem2 = rem % (a.G * n_split);
-    const int h = kvh * a.G + rem2 / n_split;
-    const int sp = rem2 % n_split;
+    const int rem2 = rem % (a.G * n_split * DS);
+    const int h = kvh * a.G + rem2 / (n_split * DS);
+    const int sp = (rem2 % (n_split * DS)) / DS;
+    const int ds = rem2 % DS;  // this workgroup's output dims: [ds * HDV, + HDV)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hh = lane >> 5;
@@ -231,8 +242,9 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     // banks once.  Consecutive dims would put lanes 8 rows apart, on two
     // banks (the row stride is 16 banks mod 32).
     constexpr int KCH = HD / 8;                   // 16-byte chunks per key row
+    constexpr int KCHV = HDV / 8;                 // 16-byte chunks of a V row slice
     constexpr int KPT = BN * KCH / 256;           // K chunks per thread
-    constexpr int VPT = (KCH * (BN / 4) + 255) / 256;  // V 4-key groups per thread
+    constexpr int VPT = (KCHV * (BN / 4) + 255) / 256;  // V 4-key groups per thread
     static_assert(BN * KCH % 256 == 0, "K tile split");
     f16x8 rk[KPT];
     f16x8 rv[VPT][4];
@@ -252,7 +264,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             if (s0 + BN > w) return false;
         }
         const f16* kb = a.k + (size_t)s0 * a.kv_dim + kvh * HD;
-        const f16* vb = a.v + (size_t)s0 * a.kv_dim + kvh * HD;
+        const f16* vb = a.v + (size_t)s0 * a.kv_dim + kvh * HD + ds * HDV;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + 256 * i;
@@ -263,7 +275,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         for (int i = 0; i < VPT; ++i) {
             const int pr = tid + 256 * i;
             const int kg = pr % (BN / 4), dc = pr / (BN / 4);
-            if (pr < KCH * (BN / 4))
+            if (pr < KCHV * (BN / 4))
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
                     rv[i][u] = *reinterpret_cast<const f16x8*>(vb + (size_t)(4 * kg + u) * a.kv_dim + dc * 8);
@@ -290,15 +302,16 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             for (int u = 0; u < 4; ++u) {
                 const int p = kt + 4 * kg + u;
                 f16x8 val = {};
-                if (pr < KCH * (BN / 4) && p >= wg_lo && p <= wg_hi)
-                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + dc * 8);
+                if (pr < KCHV * (BN / 4) && p >= wg_lo && p <= wg_hi)
+                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + ds * HDV +
+                                                          dc * 8);
                 rv[i][u] = val;
             }
         }
     };
     auto stash = [&](int stage) {
         f16* Ks = K_s + stage * (BN * KPAD);
-        f16* Vts = Vt_s + stage * (HD * VPAD);
+        f16* Vts = Vt_s + stage * (HDV * VPAD);
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + 256 * i;
@@ -308,7 +321,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int pr = tid + 256 * i;
-            if (pr >= KCH * (BN / 4)) continue;
+            if (pr >= KCHV * (BN / 4)) continue;
             const int kg = pr % (BN / 4), dc = pr / (BN / 4);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -334,7 +347,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         if (!wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
         const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
         const f16* Ks = K_s + stage * (BN * KPAD);
-        const f16* Vts = Vt_s + stage * (HD * VPAD);
+        const f16* Vts = Vt_s + stage * (HDV * VPAD);
 
         // ---- S^T - m = K Q^T - m, two 32-key blocks.  The accumulators start
         //      at -mb (mb = the running max once one is set), so the scores
@@ -452,8 +465,8 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         // the split's partial: o as accumulated, and (m, l); an empty split
         // leaves m = -1e30, l = 0, o = 0
         const size_t row = ((size_t)sp * t + qrow) * a.H + h;
-        if (hh == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * row) = f32x2{m_run, l_tot};
-        float* prow = a.part_o + row * HD;
+        if (hh == 0 && ds == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * row) = f32x2{m_run, l_tot};
+        float* prow = a.part_o + row * HD + ds * HDV;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -463,8 +476,8 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         return;
     }
     const float inv = 1.f / l_tot;
-    float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
-    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride : nullptr;
+    float* orow = a.out + ((size_t)qrow * a.H + h) * HD + ds * HDV;
+    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride + ds * HDV : nullptr;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -906,7 +919,7 @@ int decode_max_vis(const lmx_attn_params* p);
 static int prefill_splits(const lmx_attn_params* p) {
     const int hd = (int)p->head_dim;
     if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads)) return 1;
-    const long n_wg = (long)((p->n_tokens + kPfBM - 1) / kPfBM) * p->n_heads;
+    const long n_wg = (long)((p->n_tokens + kPfBM - 1) / kPfBM) * p->n_heads * (hd >= 512 ? 2 : 1);
     const long slots = (long)kCus * (hd > 128 ? 1 : 2);
     if (n_wg >= slots) return 1;
     const int bn = hd >= 256 ? 32 : 64;
@@ -930,7 +943,7 @@ size_t prefill_workspace_bytes(const lmx_attn_params* p) {
 
 bool prefill_supported(const lmx_attn_params* p, lmx_dtype q_dt) {
     (void)q_dt;
-    return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
+    return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256 || p->head_dim == 512;
 }
 
 lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
@@ -967,7 +980,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
     const int bm = pp ? kPpBM : kPfBM;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
-    const long nblk = (long)a.n_qtiles * a.H * a.n_split;
+    const long nblk = (long)a.n_qtiles * a.H * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
     if (nblk > INT_MAX) return LMX_E_SHAPE;
     dim3 grid((unsigned)nblk);
     (void)hipGetLastError();
@@ -981,11 +994,13 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
         if (hd == 64) LMX_PF(f16, 64);
         else if (hd == 128) LMX_PF(f16, 128);
         else if (hd == 256) LMX_PF(f16, 256);
+        else if (hd == 512) LMX_PF(f16, 512);
         else return LMX_E_UNSUPPORTED;
     } else {
         if (hd == 64) LMX_PF(float, 64);
         else if (hd == 128) LMX_PF(float, 128);
         else if (hd == 256) LMX_PF(float, 256);
+        else if (hd == 512) LMX_PF(float, 512);
         else return LMX_E_UNSUPPORTED;
     }
 #undef LMX_PF

@@ -249,6 +249,8 @@ def test_exact_visible_range_decode(kw):
     dict(t=256, H=8, Hkv=2, hd=128, base=1044, window=300, ring=True, k_cur=True),  # chunk on a ring
     dict(t=300, H=8, Hkv=4, hd=128, base=100, window=64, bidi=True, ring=True, k_cur=True),
     dict(t=300, H=8, Hkv=4, hd=64, base=100, bidi=True),
+    dict(t=600, H=4, Hkv=1, hd=512, base=0, window=256, ring=True, k_cur=True),  # hd 512, dim slices
+    dict(t=96, H=4, Hkv=1, hd=512, base=3000),                                    # hd 512, key splits
 ])
 def test_exact_visible_range_prefill(kw, prefill_kernel):
     exact_case(q_f16=True, **kw)
@@ -294,6 +296,7 @@ def test_exact_check_rejects_a_planted_off_by_one():
     (256, 16, 8, 2048, 0, 1024),    # Gemma SWA, past the window (k_cur)
     (256, 16, 8, 256, 7000, 0),     # a chunk on a long cache (key splits)
     (128, 32, 8, 1024, 0, 0),       # both kernels at hd 128
+    (512, 16, 1, 1024, 0, 0),       # Gemma 4 global layer shape
 ])
 def test_scale_one_qk_normed_prefill(hd, H, Hkv, t, base, window, prefill_kernel):
     say(f"scale 1.0 prefill[{prefill_kernel}] hd={hd} t={t} base={base} w={window}")

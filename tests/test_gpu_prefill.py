@@ -147,3 +147,18 @@ def test_full_size_sampled_rows(S, base):
     # every row is a convex combination of V rows: finite and bounded by max|V|
     assert np.all(np.isfinite(got))
     assert np.abs(got).max() <= np.abs(c.vf).max() + 1e-3
+
+
+@pytest.mark.parametrize("t,base", [(300, 0), (2048, 0), (64, 6000), (333, 50)])
+def test_head_dim_512_prefill(t, base):
+    """Gemma 4 global layers: head_dim 512, one kv head (ARCHITECTURE.md:25-28;
+    attn.wgsl:44-46 takes hd <= 512).  Two workgroups share each (head,
+    query tile), one per half of the output dims; a short chunk on a long
+    cache also takes key splits."""
+    c = AttnCase(512 + t + base, t=t, H=16, Hkv=1, hd=512, n_pos=base + t, q_f16=True, qk_norm=True)
+    check(c, base=base, scale=1.0 / np.sqrt(512))
+
+
+def test_head_dim_512_sliding_window_with_k_cur():
+    c = AttnCase(5120, t=700, H=8, Hkv=2, hd=512, n_pos=1700, q_f16=True)
+    check(c, base=1000, window=512, ring=True, k_cur=True, scale=1.0 / np.sqrt(512))
