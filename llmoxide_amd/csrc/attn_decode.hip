@@ -48,9 +48,14 @@ static long target_wgs(int n_q) {
     if (v > 0) return v;
     return n_q > 1 ? std::max(2048L, std::min(16384L, 256L * n_q)) : 256;
 }
-static long min_tiles_per_wave() {
-    static long v = env_long("LMX_DECODE_MIN_TILES", 2);
-    return v;
+static long min_tiles_per_wave(int hd) {
+    static long v = env_long("LMX_DECODE_MIN_TILES", 0);
+    if (v > 0) return v;
+    // A 16-key tile at head_dim >= 256 is 16 KB of K and V: one per wave puts
+    // a short window's whole read in flight at once (Gemma's 1024-key SWA
+    // layers: 128 workgroups instead of 64; 11.9 -> 10.5 us a call).  At 128
+    // two tiles a wave measured better for the 512-key C1 decode.
+    return hd >= 256 ? 1 : 2;
 }
 
 // n_q query rows (tokens or sequences), longest visible range max_vis.
@@ -65,7 +70,7 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
     const long n_tiles = (max_vis + kTile - 1) / kTile;
     const long wph = kWaves / pl.hw;
     long P = (target_wgs(n_q) + units - 1) / units;
-    const long cap = n_tiles / (wph * min_tiles_per_wave());
+    const long cap = n_tiles / (wph * min_tiles_per_wave(hd));
     if (P > cap) P = cap;
     if (P > kMaxP) P = kMaxP;
     if (P < 1) P = 1;

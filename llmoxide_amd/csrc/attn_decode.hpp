@@ -94,6 +94,9 @@ constexpr int kMergePer = 8;            // partials per merge thread
 #ifndef LMX_DEC_DEPTH_128
 #define LMX_DEC_DEPTH_128 2  // K/V tiles in flight per wave at head_dim 128
 #endif
+#ifndef LMX_DEC_DEPTH_256
+#define LMX_DEC_DEPTH_256 1  // at head_dim 256 (1: load, then compute)
+#endif
 
 // Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
 // batched: the sequence's last position).
@@ -238,11 +241,11 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     constexpr int DPL = HD / 16;  // V dims per lane
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
-    constexpr bool PIPE = HD <= 128;
+    constexpr bool PIPE = HD <= 128 || (HD == 256 && LMX_DEC_DEPTH_256 > 1);
     // Tiles in flight per wave (a 16-key tile is 16 K + 16 V registers per
     // lane at hd 128, 8 + 8 at hd 64).  At hd 128 two measured best: with
     // one wave per SIMD, deeper buffers (3, 4, 6) only lengthen the start.
-    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : LMX_DEC_DEPTH_128);
+    constexpr int DEPTH = !PIPE ? 1 : (HD <= 64 ? 4 : (HD == 256 ? LMX_DEC_DEPTH_256 : LMX_DEC_DEPTH_128));
     static_assert(GB * (SPLIT_Q ? 2 : 1) <= 16, "query columns");
     static_assert(VR * VW == DPL, "V lane layout");
     static_assert(kWaves % HW == 0, "waves per head");

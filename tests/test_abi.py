@@ -348,8 +348,10 @@ def test_noalloc_validates_and_refuses_shapes_beyond_its_scratch():
     for kw in (dict(n_slots=32768, base_pos=32767), dict(n_tokens=512, n_slots=4608, base_pos=4096)):
         assert 0 < L.lmx_attn_workspace_bytes(ctypes.byref(_params(**kw))) <= limit
     # a shape beyond the scratch is refused before anything is enqueued
-    candidates = [_params(n_tokens=t, n_heads=80, n_kv_heads=16, head_dim=hd, n_slots=8192,
-                          base_pos=8192 - t) for (t, hd) in ((1024, 512), (2048, 512), (4096, 256))]
+    # (a 896-token chunk of 73 heads on a 20k cache: 7 x 73 = 511 query-tile
+    # workgroups, cut in two key splits of 896 x 73 partial rows each)
+    candidates = [_params(n_tokens=896, n_heads=73, n_kv_heads=1, head_dim=128, n_slots=20896,
+                          base_pos=20000)]
     big = [p for p in candidates if L.lmx_attn_workspace_bytes(ctypes.byref(p)) > limit]
     assert big
     assert call(big[0]) == lmx.Status.E_WORKSPACE

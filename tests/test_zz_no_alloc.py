@@ -81,8 +81,10 @@ def test_noalloc_matches_the_workspace_entry_point(cases):
 
 def test_noalloc_refuses_a_shape_beyond_its_scratch():
     L = lmx.lib()
-    p = lmx.attn_params(n_tokens=2048, n_heads=80, n_kv_heads=16, head_dim=512, base_pos=6144,
-                        n_slots=8192)
+    # a 896-token chunk of 73 heads on a 20k cache: two key splits of 896 x 73
+    # partial rows of head_dim 128, about 68 MB
+    p = lmx.attn_params(n_tokens=896, n_heads=73, n_kv_heads=1, head_dim=128, base_pos=20000,
+                        n_slots=20896)
     assert L.lmx_attn_workspace_bytes(ctypes.byref(p)) > lmx.NOALLOC_SCRATCH_BYTES
     x = torch.zeros(16, device="cuda")
     rc = L.lmx_attn_fwd_noalloc(ctypes.byref(p), x.data_ptr(), lmx.F32, x.data_ptr(), x.data_ptr(),
