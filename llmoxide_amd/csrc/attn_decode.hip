@@ -142,21 +142,6 @@ size_t decode_batched_workspace_bytes(const lmx_attn_params* p, int n_seq, int m
     return decode_ws_upto(n_seq, (int)p->n_heads, (int)p->n_kv_heads, (int)p->head_dim, mv);
 }
 
-// Multiply-high constants for p % window over 31-bit p (Granlund-Montgomery:
-// m = floor(2^(31+l) / w) + 1 with l = ceil(log2 w) makes
-// floor(p / w) == (p * m) >> (31 + l) for every 0 <= p < 2^31).
-static void window_magic(uint32_t w, uint32_t* magic, int* shift) {
-    if (w == 0) {
-        *magic = 0;
-        *shift = 0;
-        return;
-    }
-    int l = 0;
-    while ((1ull << l) < w) ++l;
-    *magic = (uint32_t)((1ull << (31 + l)) / w + 1);
-    *shift = 31 + l;
-}
-
 static lmx_status run(DecodeArgs a, const DecodePlan& pl, int n_q, int hd, lmx_dtype q_dt,
                       int mode, void* ws, size_t ws_bytes, hipStream_t st) {
     if (pl.total() > 0) {

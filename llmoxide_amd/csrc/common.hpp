@@ -130,6 +130,27 @@ struct AttnIo {
     const float* gate;
 };
 
+// Multiply-high constants for p % window over 31-bit p (Granlund-Montgomery:
+// m = floor(2^(31+l) / w) + 1 with l = ceil(log2 w) makes
+// floor(p / w) == (p * m) >> (31 + l) for every 0 <= p < 2^31).
+inline void window_magic(uint32_t w, uint32_t* magic, int* shift) {
+    if (w == 0) {
+        *magic = 0;
+        *shift = 0;
+        return;
+    }
+    int l = 0;
+    while ((1ull << l) < w) ++l;
+    *magic = (uint32_t)((1ull << (31 + l)) / w + 1);
+    *shift = 31 + l;
+}
+
+// p % w for 0 <= p < 2^31 with the constants above.
+__device__ __forceinline__ int ring_slot(int p, int w, uint32_t magic, int shift) {
+    const uint32_t q = (uint32_t)(((uint64_t)(uint32_t)p * magic) >> shift);
+    return p - (int)q * w;
+}
+
 }  // namespace lmx
 
 // Host-side helpers shared by the entry points.
