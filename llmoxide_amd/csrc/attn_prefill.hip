@@ -1014,8 +1014,15 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     if (nblk > INT_MAX) return LMX_E_SHAPE;
     dim3 grid((unsigned)nblk);
     (void)hipGetLastError();
-    // linear addressing: no k_cur rows and every position below the window
-    const bool lin = !k_cur && (p->window == 0 || (uint64_t)p->base_pos + p->n_tokens <= p->window);
+    // Linear addressing: no k_cur rows and every position below the window;
+    // or a batch at base 0 whose every key is a k_cur row (row p of k_cur is
+    // position p), as a first windowed prefill chunk is.
+    bool lin = !k_cur && (p->window == 0 || (uint64_t)p->base_pos + p->n_tokens <= p->window);
+    if (k_cur && p->base_pos == 0) {
+        a.k = static_cast<const f16*>(k_cur);
+        a.v = static_cast<const f16*>(v_cur);
+        lin = true;
+    }
 #define LMX_PF(QT, HDV)                                                                           \
     do {                                                                                          \
         if (lin) hipLaunchKernelGGL((attn_prefill_kernel<QT, HDV, true>), grid, dim3(256), 0, st, a); \

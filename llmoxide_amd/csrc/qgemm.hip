@@ -38,8 +38,12 @@ enum GType { kGQ8_0 = 8, kGQ4K = 12, kGQ6K = 14 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#ifndef LMX_QGEMM_ROWS
+#define LMX_QGEMM_ROWS 128
+#endif
 constexpr int kGM = 64;        // tokens per workgroup
-constexpr int kGN = 128;       // weight rows per workgroup
+constexpr int kGN = LMX_QGEMM_ROWS;  // weight rows per workgroup (64 or 128)
+constexpr int kNTW = kGN / 64;       // 32-row MFMA tiles per wave
 constexpr int kGK = 128;       // weights per LDS chunk
 constexpr int kGThreads = 256;
 #ifndef LMX_QGEMM_OCC
@@ -243,7 +247,8 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
     f32x4 rx[8];
     uint32_t rw[WW];
     const int w_row = tid >> 1, w_part = tid & 1;
-    const bool w_live = r0 + w_row < a.rows;
+    const bool w_thread = w_row < kGN;  // threads past the tile's rows stage no W
+    const bool w_live = w_thread && r0 + w_row < a.rows;
     const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
     auto load_chunk = [&](int k0) {
 #pragma unroll
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
                 v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
             rx[u] = v;
         }
-        load_w<TY>(wrow, k0, w_part, rw);
+        if (w_thread) load_w<TY>(wrow, k0, w_part, rw);
     };
     auto stash_chunk = [&](int k0) {
 #pragma unroll
@@ -278,12 +283,12 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
                 if ((k4 & 7) == 0) xs_s[(k4 >> 3) * kGM + tok] = sx;
             }
         }
-        stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s, so_s);
+        if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s, so_s);
     };
 
-    f32x16 y[2];
+    f32x16 y[kNTW];
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int n = 0; n < kNTW; ++n)
 #pragma unroll
         for (int j = 0; j < 16; ++j) y[n][j] = 0.f;
 
@@ -296,9 +301,9 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
         if (ch + 1 < n_chunks) load_chunk((ch + 1) * kGK);  // in flight during the MFMAs
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            f32x16 acc[2];
+            f32x16 acc[kNTW];
 #pragma unroll
-            for (int n = 0; n < 2; ++n)
+            for (int n = 0; n < kNTW; ++n)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) acc[n][j] = 0.f;
 #pragma unroll
@@ -308,8 +313,8 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
                 const f16x8 ah = *reinterpret_cast<const f16x8*>(&xh_s[sw(xr, c)]);
                 const f16x8 al = *reinterpret_cast<const f16x8*>(&xl_s[sw(xr, c)]);
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
-                    const f16x8 b = *reinterpret_cast<const f16x8*>(&q_s[sw(64 * wn + 32 * n + l32, c)]);
+                for (int n = 0; n < kNTW; ++n) {
+                    const f16x8 b = *reinterpret_cast<const f16x8*>(&q_s[sw(32 * kNTW * wn + 32 * n + l32, c)]);
                     acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, acc[n], 0, 0, 0);
                     acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, acc[n], 0, 0, 0);
                 }
@@ -322,8 +327,8 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
                     xs[q4] = *reinterpret_cast<const f32x4*>(&xs_s[g * kGM + 32 * wm + 8 * q4 + 4 * hh]);
             }
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                const f32x2 so = so_s[(64 * wn + 32 * n + l32) * NG + g];
+            for (int n = 0; n < kNTW; ++n) {
+                const f32x2 so = so_s[(32 * kNTW * wn + 32 * n + l32) * NG + g];
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     float v = fmaf(so[0], acc[n][j], y[n][j]);
@@ -335,8 +340,8 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
     }
 
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        const int r = r0 + 64 * wn + 32 * n + l32;
+    for (int n = 0; n < kNTW; ++n) {
+        const int r = r0 + 32 * kNTW * wn + 32 * n + l32;
         if (r >= a.rows) continue;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
