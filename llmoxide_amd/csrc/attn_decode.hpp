@@ -95,7 +95,7 @@ constexpr int kMergePer = 8;            // partials per merge thread
 #define LMX_DEC_DEPTH_128 2  // K/V tiles in flight per wave at head_dim 128
 #endif
 #ifndef LMX_DEC_DEPTH_256
-#define LMX_DEC_DEPTH_256 1  // at head_dim 256 (1: load, then compute)
+#define LMX_DEC_DEPTH_256 1  // at head_dim 256
 #endif
 
 // Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
@@ -171,6 +171,11 @@ __device__ __forceinline__ f16x4 ld_stream4(const f16* p) {
 template <int HD, int MODE>
 __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
     constexpr int C4 = HD / 4;  // float4 columns of a head
+    args_in_sgprs(a.part_o, a.part_ml, a.out, a.gate, a.gate_stride, a.m_parts, a.n_q, a.H, a.P, a.tps, a.window);
+    if constexpr (MODE == kModeBatched)
+        args_in_sgprs(a.ctx_lens, a.max_ctx);
+    else
+        args_in_sgprs(a.base_pos, a.n_tokens, a.bidi);
     const int tid = threadIdx.x;
     const int parts = a.m_parts;
     const int part = tid & (parts - 1);
@@ -241,7 +246,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     constexpr int DPL = HD / 16;  // V dims per lane
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
-    constexpr bool PIPE = HD <= 128 || (HD == 256 && LMX_DEC_DEPTH_256 > 1);
+    // PIPE also at head_dim 256 with DEPTH 1: the first tile's loads go out
+    // with the query's, before its conversion (Gemma global decode 43.6 ->
+    // 41.6 us, the 1024-key window 0.6 us shorter per workgroup).
+    constexpr bool PIPE = HD <= 256;
     // Tiles in flight per wave (a 16-key tile is 16 K + 16 V registers per
     // lane at hd 128, 8 + 8 at hd 64).  At hd 128 two measured best: with
     // one wave per SIMD, deeper buffers (3, 4, 6) only lengthen the start.
@@ -250,6 +258,12 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     static_assert(VR * VW == DPL, "V lane layout");
     static_assert(kWaves % HW == 0, "waves per head");
 
+    args_in_sgprs(a.q, a.out, a.gate, a.part_o, a.part_ml, a.q_stride, a.gate_stride, a.H, a.G, a.kv_dim, a.P,
+                  a.tps, a.n_hblk, a.n_yg, a.window, a.c);
+    if constexpr (MODE == kModeBatched)
+        args_in_sgprs(a.k_ptrs, a.v_ptrs, a.ctx_lens, a.max_ctx);
+    else
+        args_in_sgprs(a.k, a.v, a.k_cur, a.v_cur, a.base_pos, a.n_tokens, a.bidi, a.w_magic, a.w_shift);
     const int bid = blockIdx.x;
     const int split = bid % a.P;
     const int yg = (bid / a.P) % a.n_yg;
