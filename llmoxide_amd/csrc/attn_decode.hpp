@@ -44,9 +44,13 @@
 // The launch boundary orders the partial stores before the merge loads; no
 // counters, so the pair can be replayed from a captured graph as is.  (A
 // single-launch form, where the last split workgroup of a unit merges it,
-// needs a device-scope release and acquire in every workgroup: on gfx950
-// those write back and invalidate the XCD's L2, and the kernel took 67 us
-// instead of 24.)
+// loses at one query row.  With device-scope fences in every workgroup
+// (L2 write-back and invalidate) the kernel took 67 us instead of 24.
+// Without them, a unit's splits must share one L2: workgroup b runs on XCD
+// b % 8, so one kv head per workgroup and per XCD; then the merge costs
+// 2.5 us instead of 4.3, but reading one head's 256-byte slice of each row
+// instead of four heads' 1 KB streams 13% slower (26.8 vs 23.7 us at the
+// Qwen3-8B 32k headline; 29.3 us a call against 27.4).)
 #pragma once
 
 #include <climits>

@@ -148,3 +148,41 @@ def test_tile_and_split_edges(ctx):
     """Context lengths around the 16-key tile and the split boundaries."""
     c = AttnCase(ctx + 5, t=1, H=32, Hkv=8, hd=128, n_pos=ctx)
     run_case(c, base=ctx - 1)
+
+
+def test_one_workspace_serves_every_entry_point():
+    """Split-K decode, a key-split prefill and the chunked delta rule keep
+    different scratch layouts in the workspace.  Interleaving the three (and
+    a second decode shape) on one workspace must give each its oracle
+    result: no call may read what another call's layout left there."""
+    import oracle
+    from tests.helpers import delta_inputs
+
+    ws = lmx.Workspace()
+    dec = AttnCase(31, t=1, H=32, Hkv=8, hd=128, n_pos=6000)
+    gem = AttnCase(32, t=1, H=16, Hkv=8, hd=256, n_pos=3000)
+    pre = AttnCase(33, t=64, H=32, Hkv=8, hd=128, n_pos=2112)
+    d_in = [(dev(c.q), dev(c.k16, torch.float16), dev(c.v16, torch.float16)) for c in (dec, gem, pre)]
+    refs = [dec.reference(base_pos=5999), gem.reference(base_pos=2999), pre.reference(base_pos=2048)]
+    conv, al, be, S0, A, dt = delta_inputs(34, T=100, n_vh=4, n_kh=2, sd=128)
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=4, n_kh=2, s_dim=128)
+    geo = [dict(n_heads=32, n_kv_heads=8, head_dim=128, base_pos=5999),
+           dict(n_heads=16, n_kv_heads=8, head_dim=256, base_pos=2999),
+           dict(n_heads=32, n_kv_heads=8, head_dim=128, base_pos=2048)]
+    for rep in range(2):
+        for i in (0, 2, 1, 0):
+            say(f"shared workspace rep={rep} attention case {i}")
+            q, kc, vc = d_in[i]
+            if i == 2:
+                out = lmx.attention(q, kc, vc, k_cur=kc[2048:], v_cur=vc[2048:], workspace=ws, **geo[i])
+            else:
+                out = lmx.attention(q, kc, vc, workspace=ws, **geo[i])
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), refs[i], what=f"rep {rep} case {i}")
+        say(f"shared workspace rep={rep} delta chunked")
+        state = dev(S0.copy())
+        o = lmx.delta_chunked(dev(conv), dev(al), dev(be), state, dev(A), dev(dt), n_vh=4, n_kh=2,
+                              s_dim=128, chunk=64, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(o.cpu().numpy(), o_ref, what="delta o")
+        assert_close(state.cpu().numpy().ravel(), S_ref, what="delta S")

@@ -53,6 +53,7 @@ def both(c: AttnCase, base: int, q_f16: bool):
     assert rc == 0, lmx.Status(rc)
     ws = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
     base_ptr = ws.data_ptr() + (-ws.data_ptr()) % 256
+    assert L.lmx_workspace_init(base_ptr, need, stream) == 0  # zeroed once before first use
     rc = L.lmx_attn_fwd(ctypes.byref(p), q.data_ptr(), qdt, kc.data_ptr(), vc.data_ptr(), lmx.F16,
                         None, None, out_ws.data_ptr(), base_ptr, need, stream)
     assert rc == 0, lmx.Status(rc)
