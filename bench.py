@@ -522,7 +522,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): this build has no "
-              "multi-GPU path; see DESIGN.md for how it would shard.", file=sys.stderr)
+              "multi-GPU path (each GPU would run these kernels on its own heads' share).",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
