@@ -13,7 +13,8 @@
 //                 each lane own one query column, so softmax is mostly in-lane)
 //
 // Two kernels share these tiles.  attn_prefill_kernel: workgroup = 4 waves x
-// 32 query rows of one query head, two workgroups per CU.  The ping-pong
+// 32 query rows, of one query head or of 2-4 heads that share a kv head
+// (head_dim >= 256), two workgroups per CU below head_dim 256.  The ping-pong
 // kernel (head_dim 128, long batches): 8 waves x 32 rows, one workgroup per
 // CU, the two waves of each SIMD kept half a tile apart so one's MFMAs run
 // beside the other's softmax.  K/V tiles of 64 keys are staged in LDS.  Key
@@ -43,6 +44,7 @@ struct PrefillArgs {
     int H, Hkv, G, kv_dim;
     int base_pos, window, n_tokens, bidi;
     int n_qtiles;
+    int gp;  // attn_prefill_kernel: query heads per workgroup (1, 2 or 4, dividing G)
     uint32_t w_magic;  // p % window == ring_slot(p, window, w_magic, w_shift)
     int w_shift;
     float c;  // scale * log2(e)
@@ -156,32 +158,39 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
     __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HDV * VPAD];
 
-    // ---- which (head, query tile, key split) this workgroup owns
+    // ---- which (heads, query tile, key split) this workgroup owns.  The gp
+    // query heads of a workgroup share kv head kvh; each takes 4 / gp waves,
+    // i.e. 128 / gp query rows.  Fewer rows per head narrow the key range a
+    // workgroup spans (a window's or the causal diagonal's spread) at the
+    // same MFMA work per K/V tile.
     const int nblk = gridDim.x;
     const int logical = xcd_remap(blockIdx.x, nblk);
     const int n_split = a.n_split;
-    const int per_kvh = a.n_qtiles * a.G * n_split * DS;
+    const int gp = a.gp, hgroups = a.G / gp;
+    const int per_kvh = a.n_qtiles * hgroups * n_split * DS;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
     // Query tiles heaviest first (causal work grows with qt).  When the whole
     // grid is resident at once (two workgroups per CU), the second half is
     // walked lightest first, so the two workgroups a CU receives pair a heavy
     // tile with a light one instead of two of nearly the same weight.
-    const int pos = rem / (a.G * n_split * DS);
+    const int pos = rem / (hgroups * n_split * DS);
     const int half = (a.n_qtiles + 1) / 2;
     const bool fold = HD <= 128 && nblk <= 2 * kPfCus;
     const int qt = (fold && pos >= half) ? pos - half : a.n_qtiles - 1 - pos;
-    const int rem2 = rem % (a.G * n_split * DS);
-    const int h = kvh * a.G + rem2 / (n_split * DS);
+    const int rem2 = rem % (hgroups * n_split * DS);
     const int sp = (rem2 % (n_split * DS)) / DS;
     const int ds = rem2 % DS;  // this workgroup's output dims: [ds * HDV, + HDV)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hh = lane >> 5;
+    const int wph = 4 / gp;             // waves per query head
+    const int bm = kPfBM / gp;          // query rows per head
+    const int h = kvh * a.G + (rem2 / (n_split * DS)) * gp + wave / wph;  // this wave's head
     const int t = a.n_tokens, base = a.base_pos, w = a.window;
     const int end = base + t - 1;
-    const int q0 = qt * kPfBM;
-    const int qw0 = q0 + wave * 32;
+    const int q0 = qt * bm;
+    const int qw0 = q0 + (wave % wph) * 32;
 
     // ---- this lane's query (column l32 of the wave's S^T tiles)
     const int qrow = qw0 + l32;
@@ -220,7 +229,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     }
 
     // ---- key ranges: the workgroup's, and this wave's
-    const int q_last = min(q0 + kPfBM, t) - 1;
+    const int q_last = min(q0 + bm, t) - 1;
     const int wg_lo = vis_lo(base + q0, w);
     const int wg_hi = vis_hi(base + q_last, w, a.bidi, end);
     const int wq_last = min(qw0 + 31, t - 1);
@@ -942,6 +951,19 @@ static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
     return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
 }
 
+// Query heads per attn_prefill_kernel workgroup.  At head_dim >= 256 two
+// heads of a kv group share a workgroup (64 rows each): a 1024-key window
+// then spans 34 key tiles per workgroup instead of 36, at the same MFMA work
+// per tile.  LMX_PREFILL_GP=1|2|4 overrides it (read on every call, for tests
+// and sweeps) where it divides G.
+static int prefill_gp(int hd, int G) {
+    if (const char* e = std::getenv("LMX_PREFILL_GP")) {
+        const int v = std::atoi(e);
+        if ((v == 1 || v == 2 || v == 4) && G % v == 0) return v;
+    }
+    return hd >= 256 && G % 2 == 0 ? 2 : 1;
+}
+
 // Key splits for attn_prefill_kernel.  When the query tiles give fewer
 // workgroups than the CUs hold at once (two per CU, one at head_dim 256), as
 // for a short chunk on a long cache, each tile's key range is cut into splits
@@ -954,13 +976,15 @@ int decode_max_vis(const lmx_attn_params* p);
 static int prefill_splits(const lmx_attn_params* p) {
     const int hd = (int)p->head_dim;
     if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads)) return 1;
-    const long n_wg = (long)((p->n_tokens + kPfBM - 1) / kPfBM) * p->n_heads * (hd >= 512 ? 2 : 1);
+    const int gp = prefill_gp(hd, (int)(p->n_heads / p->n_kv_heads));
+    const long bm = kPfBM / gp;
+    const long n_wg = (long)((p->n_tokens + bm - 1) / bm) * (p->n_heads / gp) * (hd >= 512 ? 2 : 1);
     const long slots = (long)kCus * (hd > 128 ? 1 : 2);
     if (n_wg >= slots) return 1;
     const int bn = hd >= 256 ? 32 : 64;
     // the longest key range a workgroup covers: one query's range plus the
     // spread of the tile's positions
-    const long tiles = ((long)decode_max_vis(p) + kPfBM + bn - 1) / bn + 1;
+    const long tiles = ((long)decode_max_vis(p) + bm + bn - 1) / bn + 1;
     long sp = (slots + n_wg - 1) / n_wg;
     if (sp > tiles / kMinSplitTiles) sp = tiles / kMinSplitTiles;
     if (sp > kMaxSplits) sp = kMaxSplits;
@@ -1014,9 +1038,10 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
     const int hd = (int)p->head_dim;
     const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
-    const int bm = pp ? kPpBM : kPfBM;
+    a.gp = pp ? 1 : prefill_gp(hd, a.G);
+    const int bm = pp ? kPpBM : kPfBM / a.gp;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
-    const long nblk = (long)a.n_qtiles * a.H * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
+    const long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
     if (nblk > INT_MAX) return LMX_E_SHAPE;
     dim3 grid((unsigned)nblk);
     (void)hipGetLastError();

@@ -102,6 +102,24 @@ def test_prefill_head_geometries(H, Hkv, hd):
     check(c, base=50, scale=1.0 / np.sqrt(hd))
 
 
+@pytest.mark.parametrize("gp", [1, 2, 4])
+@pytest.mark.parametrize("H,Hkv,hd,window", [(16, 4, 128, 0), (16, 4, 128, 150), (8, 2, 256, 0),
+                                             (16, 8, 256, 300)])
+def test_prefill_heads_per_workgroup(gp, H, Hkv, hd, window, monkeypatch):
+    """Query heads of one kv group packed into a workgroup (128 / gp rows
+    each): ragged t, a window, and a ring with k_cur rows, against the oracle.
+    gp = 4 only where it divides G."""
+    if (H // Hkv) % gp:
+        pytest.skip("gp must divide the group size")
+    monkeypatch.setenv("LMX_PREFILL_GP", str(gp))
+    c = AttnCase(gp * 1000 + H + hd + window, t=333, H=H, Hkv=Hkv, hd=hd, n_pos=333 + 400, q_f16=True)
+    say(f"heads per workgroup gp={gp}")
+    if window:
+        check(c, base=400, window=window, ring=True, k_cur=True, scale=1.0 / np.sqrt(hd))
+    else:
+        check(c, base=400, scale=1.0 / np.sqrt(hd))
+
+
 def test_gemma_swa_prefill_first_window():
     """Gemma-shape SWA layer (hd 256, w 1024, scale 1/16) in the reference's
     self-consistent regime (base + t <= window): reads the ring."""
