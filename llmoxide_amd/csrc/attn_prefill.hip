@@ -591,13 +591,14 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];
     __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
 
+    // The workgroup's gp query heads share kv head kvh, 256 / gp rows each.
     const int nblk = gridDim.x;
     const int logical = xcd_remap(blockIdx.x, nblk);
-    const int per_kvh = a.n_qtiles * a.G;
+    const int gp = a.gp, hgroups = a.G / gp;
+    const int per_kvh = a.n_qtiles * hgroups;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
-    const int qt = a.n_qtiles - 1 - rem / a.G;
-    const int h = kvh * a.G + (rem % a.G);
+    const int qt = a.n_qtiles - 1 - rem / hgroups;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -606,10 +607,13 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     const int l32 = lane & 31, hh = lane >> 5;
     const int t = a.n_tokens, base = a.base_pos, w = a.window;
     const int end = base + t - 1;
-    const int q0 = qt * kPpBM;
+    const int bm = kPpBM / gp;  // query rows per head
+    const int q0 = qt * bm;
     // The groups take alternate 32-row blocks, so the two waves of a SIMD
-    // have nearly the same causal key range.
-    const int qw0 = q0 + 32 * (2 * (wave & 3) + grp);
+    // have nearly the same causal key range (and, with gp = 4, one head).
+    const int blk = 2 * (wave & 3) + grp, bph = 8 / gp;  // 32-row blocks per head
+    const int h = kvh * a.G + (rem % hgroups) * gp + blk / bph;
+    const int qw0 = q0 + 32 * (blk % bph);
 
     const int qrow = qw0 + l32;
     const bool qvalid = qrow < t;
@@ -643,7 +647,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     }
 
     // ---- key tiles of the workgroup, and the wave's own run of them
-    const int q_last = min(q0 + kPpBM, t) - 1;
+    const int q_last = min(q0 + bm, t) - 1;
     const int wg_lo = vis_lo(base + q0, w);
     const int wg_hi = vis_hi(base + q_last, w, a.bidi, end);
     const int kt_begin = (wg_lo / BN) * BN;
@@ -951,16 +955,17 @@ static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
     return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
 }
 
-// Query heads per attn_prefill_kernel workgroup.  At head_dim >= 256 two
-// heads of a kv group share a workgroup (64 rows each): a 1024-key window
-// then spans 34 key tiles per workgroup instead of 36, at the same MFMA work
-// per tile.  LMX_PREFILL_GP=1|2|4 overrides it (read on every call, for tests
-// and sweeps) where it divides G.
-static int prefill_gp(int hd, int G) {
+// Query heads per prefill workgroup (they share one kv head).  At head_dim
+// >= 256 two heads of a kv group share a workgroup (64 rows each): a
+// 1024-key window then spans 34 key tiles per workgroup instead of 36, at
+// the same MFMA work per tile.  LMX_PREFILL_GP=1|2|4 overrides it (read on
+// every call, for tests and sweeps) where it divides G.
+static int prefill_gp(int hd, int G, bool pp) {
     if (const char* e = std::getenv("LMX_PREFILL_GP")) {
         const int v = std::atoi(e);
         if ((v == 1 || v == 2 || v == 4) && G % v == 0) return v;
     }
+    if (pp) return 1;
     return hd >= 256 && G % 2 == 0 ? 2 : 1;
 }
 
@@ -976,7 +981,7 @@ int decode_max_vis(const lmx_attn_params* p);
 static int prefill_splits(const lmx_attn_params* p) {
     const int hd = (int)p->head_dim;
     if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads)) return 1;
-    const int gp = prefill_gp(hd, (int)(p->n_heads / p->n_kv_heads));
+    const int gp = prefill_gp(hd, (int)(p->n_heads / p->n_kv_heads), false);
     const long bm = kPfBM / gp;
     const long n_wg = (long)((p->n_tokens + bm - 1) / bm) * (p->n_heads / gp) * (hd >= 512 ? 2 : 1);
     const long slots = (long)kCus * (hd > 128 ? 1 : 2);
@@ -1038,8 +1043,8 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
     const int hd = (int)p->head_dim;
     const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
-    a.gp = pp ? 1 : prefill_gp(hd, a.G);
-    const int bm = pp ? kPpBM : kPfBM / a.gp;
+    a.gp = prefill_gp(hd, a.G, pp);
+    const int bm = (pp ? kPpBM : kPfBM) / a.gp;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
     const long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
     if (nblk > INT_MAX) return LMX_E_SHAPE;
