@@ -25,6 +25,8 @@ static int pick_hw(int Hkv) {
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+constexpr long kCusPerGpu = 256;  // compute units of the target (MI355X)
+
 static long env_long(const char* name, long dflt) {
     const char* e = std::getenv(name);
     const long x = e ? std::atol(e) : 0;
@@ -58,8 +60,22 @@ static long min_tiles_per_wave(int hd) {
     return hd >= 256 ? 1 : 2;
 }
 
+// K row-major through LDS (head_dim 128), or each lane's operand bytes
+// loaded directly.  Rows pay wherever the LDS round trip it adds to a tile is
+// hidden: by other workgroups on the CU (ragged batches: B=8 116 -> 108 us,
+// B=32 358 -> 336 us) or by a short stream (the 512-key C1 decode, 2 tiles a
+// wave: 8.05 -> 7.73 us).  One workgroup per CU streaming 16 tiles a wave
+// (B=1 at 32k) keeps the direct loads, 1% faster there (27.1 against 27.5 us
+// a call).  LMX_DECODE_KROWS=0|1 forces it (read on every call, for tests).
+static bool pick_krows(int hd, int mode, const DecodePlan& pl) {
+    if (hd != 128) return false;
+    if (const char* e = std::getenv("LMX_DECODE_KROWS")) return e[0] == '1';
+    const int tiles_per_wave = (pl.tps + kWaves / pl.hw - 1) / (kWaves / pl.hw);
+    return mode == kModeBatched || pl.n_main > kCusPerGpu || tiles_per_wave <= 4;
+}
+
 // n_q query rows (tokens or sequences), longest visible range max_vis.
-static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
+static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis, int mode) {
     DecodePlan pl{};
     const int G = H / Hkv;
     pl.gb = pick_gb(G, hd);
@@ -97,6 +113,7 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
         pl.ml_bytes = round_up((size_t)n_q * H * P * 2 * 4, 256);
         pl.o_bytes = round_up((size_t)n_q * H * P * hd * 4, 256);
     }
+    pl.krows = pick_krows(hd, mode, pl);
     if (pl.P_ws > 1)
         pl.ws_bytes = round_up((size_t)n_q * H * pl.P_ws * 2 * 4, 256) +
                       round_up((size_t)n_q * H * pl.P_ws * hd * 4, 256);
@@ -109,7 +126,7 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis) {
 // as rows are added, and n_q * P can dip when it does).
 static size_t decode_ws_upto(int n_q, int H, int Hkv, int hd, int max_vis) {
     size_t need = 0;
-    for (int n = 1; n <= n_q; ++n) need = std::max(need, plan_decode(n, H, Hkv, hd, max_vis).ws_bytes);
+    for (int n = 1; n <= n_q; ++n) need = std::max(need, plan_decode(n, H, Hkv, hd, max_vis, kModeGeneral).ws_bytes);
     return need;
 }
 
@@ -199,13 +216,13 @@ lmx_status decode_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q,
     a.bidi = (int)p->bidi;
     a.c = p->scale * kLog2e;
     const int mv = decode_max_vis(p);
-    const DecodePlan pl = plan_decode(a.n_tokens, a.H, a.Hkv, (int)p->head_dim, mv);
     // Linear addressing reads row p for every visible p: no k_cur rows and no
     // ring wrap (every visible position is below the window).
     const long last = (long)p->base_pos + p->n_tokens - 1;
     const bool linear = !k_cur && (p->window == 0 || last < (long)p->window);
-    return run(a, pl, a.n_tokens, (int)p->head_dim, q_dt, linear ? kModeLinear : kModeGeneral, ws,
-               ws_bytes, st);
+    const int mode = linear ? kModeLinear : kModeGeneral;
+    const DecodePlan pl = plan_decode(a.n_tokens, a.H, a.Hkv, (int)p->head_dim, mv, mode);
+    return run(a, pl, a.n_tokens, (int)p->head_dim, q_dt, mode, ws, ws_bytes, st);
 }
 
 lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, const int32_t* ctx_lens,
@@ -228,7 +245,7 @@ lmx_status decode_batched(const lmx_attn_params* p, int n_seq, int max_ctx, cons
     a.c = p->scale * kLog2e;
     int mv = max_ctx;
     if (a.window && a.window < mv) mv = a.window;
-    const DecodePlan pl = plan_decode(n_seq, a.H, a.Hkv, (int)p->head_dim, mv);
+    const DecodePlan pl = plan_decode(n_seq, a.H, a.Hkv, (int)p->head_dim, mv, kModeBatched);
     return run(a, pl, n_seq, (int)p->head_dim, q_dt, kModeBatched, ws, ws_bytes, st);
 }
 

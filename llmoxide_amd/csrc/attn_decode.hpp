@@ -243,10 +243,15 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(DecodeArgs a) {
     }
 }
 
-template <typename QT, int HD, int GB, int HW, int MODE>
+template <typename QT, int HD, int GB, int HW, int MODE, bool KR>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) {
     using Tile = KVTile<HD>;
     constexpr int KS = Tile::KS, VR = Tile::VR, VW = Tile::VW;
+    // KR (head_dim 128): K loaded row-major, as V, and turned into MFMA
+    // operands through LDS, so that each load instruction reads four whole
+    // 256-byte rows instead of 64 bytes of sixteen rows.  The launch picks it
+    // (pick_krows); without it each lane loads its operand bytes directly.
+    constexpr bool KROWS = KR && HD == 128;
     constexpr int DPL = HD / 16;  // V dims per lane
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
@@ -321,9 +326,17 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     // clamped to hi (their scores are masked).
     auto load_tile = [&](int t, Tile& b) {
         const int kt = lo + kTile * t;
-        const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
+        if constexpr (KROWS) {
+            // K as V: load i, lane (g4, c16) holds key 4 g4 + i, dims
+            // 8 c16 .. + 7 (one 256-byte row per 16 lanes)
 #pragma unroll
-        for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8(krow + 32 * s + 8 * g4);
+            for (int i = 0; i < KS; ++i)
+                b.k[i] = ld_stream8(row_ptr(kc, a.k_cur, min(kt + 4 * g4 + i, hi)) + 8 * c16);
+        } else {
+            const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
+#pragma unroll
+            for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8(krow + 32 * s + 8 * g4);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f16* vrow = row_ptr(vc, a.v_cur, min(kt + 4 * g4 + i, hi));
@@ -350,6 +363,9 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     __shared__ float sm_l[kWaves][GB];
     // Per-wave LDS slots: p[key][head] and corr[group][head] of the tile.
     __shared__ __attribute__((aligned(16))) float P_s[kWaves][kTile][8];
+    // KROWS: the K tile, rows of HD + 8 halfs (the operand reads of 16 rows
+    // then fall on distinct banks).
+    __shared__ __attribute__((aligned(16))) f16 K_s[KROWS ? kWaves : 1][kTile][KROWS ? HD + 8 : 8];
     __shared__ __attribute__((aligned(16))) float C_s[kWaves][4][8];
 
     // Combine the WPH waves of each head slot (after a workgroup barrier):
@@ -459,9 +475,24 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         auto compute_tile = [&](int t, const Tile& b) {
             const int kt = lo + kTile * t;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (KROWS) {
+                // Row-major K tile through this wave's LDS slice, read back
+                // as the MFMA A operand (key c16, dims 32 s + 8 g4 .. + 7).
 #pragma unroll
-            for (int s = 0; s < KS; ++s)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], qf[s], acc, 0, 0, 0);
+                for (int i = 0; i < KS; ++i)
+                    *reinterpret_cast<f16x8*>(&K_s[wave][4 * g4 + i][8 * c16]) = b.k[i];
+                wave_lds_sync();
+                f16x8 ka[KS];
+#pragma unroll
+                for (int s = 0; s < KS; ++s) ka[s] = *reinterpret_cast<const f16x8*>(&K_s[wave][c16][32 * s + 8 * g4]);
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qf[s], acc, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], qf[s], acc, 0, 0, 0);
+            }
             float x[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -656,18 +687,26 @@ struct DecodePlan {
     int P_ws;          // splits the workspace is sized for (>= P)
     int n_main, n_yg;
     int n_merge, m_parts;
+    bool krows;                // head_dim 128: K row-major through LDS (attn_decode_kernel's KR)
     size_t ml_bytes, o_bytes;  // what this launch uses
     size_t ws_bytes;           // what the workspace query reports for this shape
     size_t total() const { return ml_bytes + o_bytes; }
 };
 
 template <typename QT, int MODE, int HW>
-inline lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, dim3 grid, hipStream_t st) {
-#define LMX_DEC_CASE(HDV, GBV)                                                                     \
-    if (hd == HDV && gb == GBV) {                                                                  \
-        hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE>), grid, dim3(kDecThreads), \
-                           0, st, a);                                                              \
-        return LMX_OK;                                                                             \
+inline lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, bool krows, dim3 grid, hipStream_t st) {
+#define LMX_DEC_CASE(HDV, GBV)                                                                        \
+    if (hd == HDV && gb == GBV) {                                                                     \
+        if constexpr (HDV == 128) {                                                                   \
+            if (krows) {                                                                              \
+                hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE, true>), grid,          \
+                                   dim3(kDecThreads), 0, st, a);                                      \
+                return LMX_OK;                                                                        \
+            }                                                                                         \
+        }                                                                                             \
+        hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE, false>), grid, dim3(kDecThreads), \
+                           0, st, a);                                                                 \
+        return LMX_OK;                                                                                \
     }
     LMX_DEC_CASE(64, 1) LMX_DEC_CASE(64, 2) LMX_DEC_CASE(64, 3) LMX_DEC_CASE(64, 4)
     LMX_DEC_CASE(64, 5) LMX_DEC_CASE(64, 6) LMX_DEC_CASE(64, 7) LMX_DEC_CASE(64, 8)
@@ -680,12 +719,12 @@ inline lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, dim3 gri
 }
 
 template <typename QT, int MODE>
-inline lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, int hw, dim3 grid,
+inline lmx_status launch_decode(const DecodeArgs& a, int hd, int gb, int hw, bool krows, dim3 grid,
                                 hipStream_t st) {
     switch (hw) {
-        case 4: return launch_decode_hw<QT, MODE, 4>(a, hd, gb, grid, st);
-        case 2: return launch_decode_hw<QT, MODE, 2>(a, hd, gb, grid, st);
-        default: return launch_decode_hw<QT, MODE, 1>(a, hd, gb, grid, st);
+        case 4: return launch_decode_hw<QT, MODE, 4>(a, hd, gb, krows, grid, st);
+        case 2: return launch_decode_hw<QT, MODE, 2>(a, hd, gb, krows, grid, st);
+        default: return launch_decode_hw<QT, MODE, 1>(a, hd, gb, krows, grid, st);
     }
 }
 
@@ -704,7 +743,7 @@ inline lmx_status launch_merge(const DecodeArgs& a, int hd, dim3 grid, hipStream
 // Enqueue the split kernel and, with more than one split, the merge kernel.
 template <typename QT, int MODE>
 lmx_status launch_mode(const DecodeArgs& a, const DecodePlan& pl, int hd, hipStream_t st) {
-    lmx_status s = launch_decode<QT, MODE>(a, hd, pl.gb, pl.hw, dim3((unsigned)pl.n_main), st);
+    lmx_status s = launch_decode<QT, MODE>(a, hd, pl.gb, pl.hw, pl.krows, dim3((unsigned)pl.n_main), st);
     if (s != LMX_OK || pl.P == 1) return s;
     return launch_merge<MODE>(a, hd, dim3((unsigned)pl.n_merge), st);
 }
