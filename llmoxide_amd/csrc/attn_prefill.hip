@@ -529,6 +529,329 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         }
 }
 
+// Short batches from linear caches (a grid of 128-row tiles would leave
+// half the CUs idle, as S = 512 at 32 heads does): a workgroup takes 64
+// query rows of one head, and its two wave pairs walk the two halves of the
+// workgroup's key tiles at once, each pair with its own two-stage K/V ring
+// (128 threads copy a pair's tile), then merge through LDS.  The heaviest
+// workgroup's serial chain of key tiles is halved (S = 512: 256 workgroups,
+// at most 4 tiles each).  Wave w: rows 32 (w & 1) .. + 31, key half w >> 1.
+// The per-tile step (scores, mask, online softmax, P.V) is attn_prefill_kernel's.
+template <typename QT, int HD>
+__global__ __launch_bounds__(256, 1) void attn_prefill_kh_kernel(PrefillArgs a) {
+    static_assert(HD <= 128, "head_dim <= 128");
+    constexpr bool kExact = sizeof(QT) == 2;
+    constexpr int BN = 64;
+    constexpr int HDV = HD;
+    constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
+    constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
+    constexpr int NB = HD / 32;      // 32-dim output blocks
+    constexpr int KPAD = HD + 8;
+    constexpr int VPAD = BN + 4;
+    constexpr int KCH = HD / 8;                         // 16-byte chunks per key row
+    constexpr int KPT = BN * KCH / 128;                 // K chunks per thread of a pair
+    constexpr int VPT = (KCH * (BN / 4) + 127) / 128;   // V 4-key groups per thread of a pair
+    static_assert(BN * KCH % 128 == 0, "K tile split");
+    __shared__ __attribute__((aligned(16))) f16 K_s[2][2][BN * KPAD];   // [pair][stage]
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[2][2][HD * VPAD];
+
+    const int nblk = gridDim.x;
+    const int logical = xcd_remap(blockIdx.x, nblk);
+    const int per_kvh = a.n_qtiles * a.G;
+    const int kvh = logical / per_kvh;
+    const int rem = logical - kvh * per_kvh;
+    const int qt = a.n_qtiles - 1 - rem / a.G;  // heaviest first
+    const int h = kvh * a.G + rem % a.G;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pair = wave >> 1, rb = wave & 1;  // key half, row block
+    const int ptid = tid & 127;                 // thread within the pair
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int t = a.n_tokens, base = a.base_pos, w = a.window;
+    const int end = base + t - 1;
+    const int q0 = qt * 64;
+    const int qw0 = q0 + 32 * rb;
+
+    const int qrow = qw0 + l32;
+    const bool qvalid = qrow < t;
+    const int qpos = base + qrow;
+    const int my_lo = qvalid ? vis_lo(qpos, w) : 1;
+    const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
+
+    f16x8 qf[KSTEPS];
+    {
+        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            float x[8];
+            if constexpr (sizeof(QT) == 2) {
+                const f16x8 q8 = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qoff + ks * 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = (float)q8[j];
+            } else {
+                const float* qp = reinterpret_cast<const float*>(a.q) + qoff + ks * 16;
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[j] = x0[j];
+                    x[4 + j] = x1[j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
+        }
+    }
+
+    // ---- key ranges: the workgroup's, and this wave's
+    const int q_last = min(q0 + 64, t) - 1;
+    const int wg_lo = vis_lo(base + q0, w);
+    const int wg_hi = vis_hi(base + q_last, w, a.bidi, end);
+    const int wq_last = min(qw0 + 31, t - 1);
+    const bool wave_live = qw0 < t;
+    const int wv_lo = wave_live ? vis_lo(base + qw0, w) : 1;                    // smallest lo
+    const int wv_hi = wave_live ? vis_hi(base + wq_last, w, a.bidi, end) : 0;  // largest hi
+    const int wv_lo_max = wave_live ? vis_lo(base + wq_last, w) : 0;          // largest lo
+    const int wv_hi_min = wave_live ? vis_hi(base + qw0, w, a.bidi, end) : -1; // smallest hi
+
+    float m_run = -1e30f, l_run = 0.f;
+    f32x16 o[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[nb][i] = 0.f;
+
+    // ---- this pair's K/V tiles (linear addressing: key p is row p); rows
+    // outside [wg_lo, wg_hi] are zero.  Same layouts as attn_prefill_kernel.
+    f16x8 rk[KPT];
+    f16x8 rv[VPT][4];
+    auto fetch = [&](int kt) {
+        const bool inside = kt >= wg_lo && kt + BN - 1 <= wg_hi;
+        const f16* kb = a.k + (size_t)kvh * HD;
+        const f16* vb = a.v + (size_t)kvh * HD;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = ptid + 128 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            const int p = kt + key;
+            f16x8 val = {};
+            if (inside || (p >= wg_lo && p <= wg_hi))
+                val = *reinterpret_cast<const f16x8*>(kb + (size_t)p * a.kv_dim + col * 8);
+            rk[i] = val;
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = ptid + 128 * i;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int p = kt + 4 * kg + u;
+                f16x8 val = {};
+                if (pr < KCH * (BN / 4) && (inside || (p >= wg_lo && p <= wg_hi)))
+                    val = *reinterpret_cast<const f16x8*>(vb + (size_t)p * a.kv_dim + dc * 8);
+                rv[i][u] = val;
+            }
+        }
+    };
+    auto stash = [&](int stage) {
+        f16* Ks = K_s[pair][stage];
+        f16* Vts = Vt_s[pair][stage];
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = ptid + 128 * i;
+            const int key = c / KCH, col = c - key * KCH;
+            *reinterpret_cast<f16x8*>(&Ks[key * KPAD + col * 8]) = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pr = ptid + 128 * i;
+            if (pr >= KCH * (BN / 4)) continue;
+            const int kg = pr % (BN / 4), dc = pr / (BN / 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<f16x4*>(&Vts[(dc * 8 + j) * VPAD + 4 * kg]) =
+                    f16x4{rv[i][0][j], rv[i][1][j], rv[i][2][j], rv[i][3][j]};
+        }
+    };
+
+    // The workgroup's tiles, first half to pair 0 and second to pair 1; both
+    // pairs take `half` steps (the second may idle on its last), one
+    // workgroup barrier each.
+    const int kt_all = (wg_lo / BN) * BN;
+    const int n_t_all = wg_lo <= wg_hi ? (wg_hi - kt_all) / BN + 1 : 0;
+    const int half = (n_t_all + 1) / 2;
+    const int first = pair * half;
+    const int my_n = min(n_t_all, first + half) - first;  // tiles of this pair (>= 0)
+    if (my_n > 0) fetch(kt_all + first * BN);
+    for (int st = 0; st < half; ++st) {
+        const int stage = st & 1;
+        const int kt = kt_all + (first + st) * BN;
+        const bool live = st < my_n;  // pair-uniform
+        // Stage `stage` was last read two steps ago, before the barrier of
+        // the previous step: writing it now needs no extra barrier.
+        if (live) stash(stage);
+        __syncthreads();
+        if (st + 1 < my_n) fetch(kt + BN);
+        if (!live || !wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
+        const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
+        const f16* Ks = K_s[pair][stage];
+        const f16* Vts = Vt_s[pair][stage];
+
+        // ---- S^T - m = K Q^T - m, two 32-key blocks.  The accumulators start
+        //      at -mb (mb = the running max once one is set), so the scores
+        //      come out already shifted for exp2.
+        float mb = m_run > -1e29f ? m_run : 0.f;
+        f32x16 s[KB];
+        qk_tile<HD, KB, KPAD, kExact>(Ks, qf, s, mb, a.c, l32, hh);
+
+        // ---- mask, online softmax.  s[kb][i] is key
+        //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
+        if (need_mask) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kt + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                    if (key < my_lo || key > my_hi) s[kb][i] = -INFINITY;
+                }
+        }
+        // The tile in two halves of 32 keys (kb), each with its own softmax
+        // step, so that the P.V MFMAs of half 0 can run while half 1's p is
+        // formed.  P^T of a half is the B operand of two 16-key k-steps,
+        // registers 0..7 and 8..15 of s[kb].  p = exp2(s) is formed first; the
+        // lazy rescale then only asks whether some p exceeds 2^slack (a score
+        // above m_run + slack), which a packed f16 max over the rounded p
+        // answers with a quarter of the instructions of a float max over the
+        // scores.  Such a half, and a query's first one (m_run not set yet),
+        // take the exact path: the float max, the rescale of o and l, and p
+        // again.
+        constexpr float kSlackP = 256.f;  // 2^kRescaleSlack
+        static_assert(kRescaleSlack == 8.f, "kSlackP is 2^kRescaleSlack");
+        const f16x2 one2 = {(f16)1.f, (f16)1.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            f16x8 pf[2];
+            auto make_p = [&]() {
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pf[st][j] = (f16)fast_exp2(s[kb][8 * st + j]);
+            };
+            make_p();
+            f16x2 pm = {pf[0][0], pf[0][1]};
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) pm = __builtin_elementwise_max(pm, f16x2{pf[st][j], pf[st][j + 1]});
+            // The test is "some p of the wave exceeds 2^slack": a ballot over
+            // each lane's own p, no combine of a query's two half-columns.
+            const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+            if (__builtin_amdgcn_ballot_w64(!(pmax <= kSlackP) || m_run < -1e29f) != 0) {
+                float mt = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[kb][i]);
+                mt = fmaxf(mt, shfl_xor(mt, 32)) + mb;  // the half's largest score
+                const float mn = fmaxf(m_run, mt);
+                const float corr = fast_exp2(m_run - mn);
+                m_run = mn;
+                l_run *= corr;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[nb][i] *= corr;
+                // The scores still to come in this tile become relative to
+                // mn; while a query has seen no key (a masked half, m_run
+                // still unset) they stay relative to 0.
+                const float nmb = mn > -1e29f ? mn : 0.f;
+                const float shift = nmb - mb;
+#pragma unroll
+                for (int k2 = kb; k2 < KB; ++k2)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[k2][i] -= shift;
+                mb = nmb;
+                make_p();
+            }
+            // The row sum takes the f16-rounded p, as the P.V product does,
+            // two at a time (v_dot2_f32_f16 against 1).
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2)
+                    l_run = __builtin_amdgcn_fdot2(f16x2{pf[st][j], pf[st][j + 1]}, one2, l_run, false);
+
+            // ---- O^T += V^T P^T.  A operand row = dim nb*32 + l32; keys
+            //      32*kb + 16*st + 4*hh + {0..3} and + 8 + 4*hh + {0..3}.
+            //      Later blocks' operands are read while block nb's MFMAs run.
+            auto load = [&](int nb, f16x8 (&va)[2]) {
+                const f16* vrow = &Vts[(nb * 32 + l32) * VPAD + 32 * kb + 4 * hh];
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow + 16 * st);
+                    const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16 * st + 8);
+                    va[st] = f16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                }
+            };
+            // Operands PVD blocks ahead: 2 at head_dim >= 256, where one wave
+            // per SIMD waits out each LDS round trip (+1.2% on Gemma's 4k
+            // prefill; 3 measured the same), 1 below.
+            constexpr int PVD = HD >= 256 ? 2 : 1;
+            static_assert(PVD < NB, "operand ring");
+            f16x8 va[PVD + 1][2];
+#pragma unroll
+            for (int d0 = 0; d0 < PVD; ++d0) load(d0, va[d0]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if (nb + PVD < NB) load(nb + PVD, va[(nb + PVD) % (PVD + 1)]);
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[nb % (PVD + 1)][st], pf[st], o[nb], 0, 0, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then two LDS reads
+                }
+            }
+        }
+    }
+
+    // ---- merge the two key halves of each row block through LDS (the K
+    // stages, free after this barrier): pair 1 writes its o, max and row sum
+    // lane-contiguous; pair 0 rescales both to the larger max and stores.
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    __syncthreads();
+    constexpr int MW = NB * 16 + 2;  // floats a lane hands over
+    static_assert(2 * MW * 64 * 4 <= (int)sizeof(K_s), "merge space");
+    float* xs = reinterpret_cast<float*>(&K_s[0][0][0]) + rb * MW * 64;
+    if (pair == 1) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xs[(nb * 16 + i) * 64 + lane] = o[nb][i];
+        xs[(NB * 16) * 64 + lane] = m_run;
+        xs[(NB * 16 + 1) * 64 + lane] = l_tot;
+    }
+    __syncthreads();
+    if (pair == 1 || !qvalid) return;
+    const float m2 = xs[(NB * 16) * 64 + lane], l2 = xs[(NB * 16 + 1) * 64 + lane];
+    const float mn = fmaxf(m_run, m2);
+    const float c0 = fast_exp2(m_run - mn), c1 = fast_exp2(m2 - mn);
+    const float inv = 1.f / (l_tot * c0 + l2 * c1);
+    float* orow = a.out + ((size_t)qrow * a.H + h) * HD;
+    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride : nullptr;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = nb * 32 + 8 * g4 + 4 * hh;
+            f32x4 y;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * g4 + j;
+                y[j] = (o[nb][i] * c0 + xs[(nb * 16 + i) * 64 + lane] * c1) * inv;
+            }
+            if (grow) y = gate_sigmoid4(y, grow + d);
+            *reinterpret_cast<f32x4*>(orow + d) = y;
+        }
+}
+
 // Combines the n_split partials of each (query row, head): with M the largest
 // split max, out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, splits in
 // order, then the output gate.  One thread per 4 output dims.
@@ -1046,10 +1369,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     a.gp = prefill_gp(hd, a.G, pp);
     const int bm = (pp ? kPpBM : kPfBM) / a.gp;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
-    const long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
-    if (nblk > INT_MAX) return LMX_E_SHAPE;
-    dim3 grid((unsigned)nblk);
-    (void)hipGetLastError();
+    long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
     // Linear addressing: no k_cur rows and every position below the window;
     // or a batch at base 0 whose every key is a k_cur row (row p of k_cur is
     // position p), as a first windowed prefill chunk is.
@@ -1059,6 +1379,19 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
         a.v = static_cast<const f16*>(v_cur);
         lin = true;
     }
+    // Key halves in one workgroup (attn_prefill_kh_kernel) when the 128-row
+    // grid would fill at most half the CUs.  LMX_PREFILL_KH=0 turns it off
+    // (read on every call, for tests and A/B timing).
+    const char* kh_env = std::getenv("LMX_PREFILL_KH");
+    const bool kh = !pp && hd <= 128 && lin && a.n_split == 1 && a.gp == 1 && 2 * nblk <= kPfCus &&
+                    !(kh_env && kh_env[0] == '0');
+    if (kh) {
+        a.n_qtiles = (a.n_tokens + 63) / 64;
+        nblk = (long)a.n_qtiles * a.H;
+    }
+    if (nblk > INT_MAX) return LMX_E_SHAPE;
+    dim3 grid((unsigned)nblk);
+    (void)hipGetLastError();
 #define LMX_PF(QT, HDV)                                                                           \
     do {                                                                                          \
         if (lin) hipLaunchKernelGGL((attn_prefill_kernel<QT, HDV, true>), grid, dim3(256), 0, st, a); \
@@ -1069,7 +1402,16 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
         if (lin) hipLaunchKernelGGL((attn_prefill_pp_kernel<QT, 128, true>), grid, dim3(512), 0, st, a); \
         else hipLaunchKernelGGL((attn_prefill_pp_kernel<QT, 128, false>), grid, dim3(512), 0, st, a);   \
     } while (0)
-    if (pp) {
+    if (kh) {
+        const bool f16q = q_dt == LMX_F16;
+        if (hd == 64) {
+            if (f16q) hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 64>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill_kh_kernel<float, 64>), grid, dim3(256), 0, st, a);
+        } else {
+            if (f16q) hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 128>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((attn_prefill_kh_kernel<float, 128>), grid, dim3(256), 0, st, a);
+        }
+    } else if (pp) {
         if (q_dt == LMX_F16)
             LMX_PP(f16);
         else

@@ -180,3 +180,22 @@ def test_head_dim_512_prefill(t, base):
 def test_head_dim_512_sliding_window_with_k_cur():
     c = AttnCase(5120, t=700, H=8, Hkv=2, hd=512, n_pos=1700, q_f16=True)
     check(c, base=1000, window=512, ring=True, k_cur=True, scale=1.0 / np.sqrt(512))
+
+
+@pytest.mark.parametrize("kh", ["1", "0"])
+@pytest.mark.parametrize("H,Hkv,hd,t,base,window,bidi,kcur,qf16", [
+    (32, 8, 128, 512, 0, 0, False, False, True),   # C3 S = 512
+    (16, 4, 64, 200, 0, 0, False, False, True),
+    (8, 2, 128, 333, 100, 0, False, False, False),  # a linear cache with rows before the batch
+    (8, 4, 128, 300, 0, 256, False, True, True),    # a windowed first chunk, keys from k_cur
+    (8, 4, 64, 250, 0, 0, True, False, True),       # bidirectional
+    (16, 4, 128, 9, 0, 0, False, False, True),      # fewer rows than a tile
+])
+def test_key_halves_prefill(kh, H, Hkv, hd, t, base, window, bidi, kcur, qf16, monkeypatch):
+    """Short batches: each workgroup's two wave pairs walk the two halves of
+    its key tiles and merge through LDS (kh=1), against the oracle; kh=0 is
+    the one-chain kernel on the same inputs."""
+    monkeypatch.setenv("LMX_PREFILL_KH", kh)
+    c = AttnCase(t + base + hd + window, t=t, H=H, Hkv=Hkv, hd=hd, n_pos=base + t, q_f16=qf16,
+                 qk_norm=True)
+    check(c, base=base, window=window, bidi=bidi, ring=kcur, k_cur=kcur)
