@@ -12,12 +12,14 @@
 //                 S^T accumulators (no shuffle: computing the transpose makes
 //                 each lane own one query column, so softmax is mostly in-lane)
 //
-// Two kernels share these tiles.  attn_prefill_kernel: workgroup = 4 waves x
+// Three kernels share these tiles.  attn_prefill_kernel: workgroup = 4 waves x
 // 32 query rows, of one query head or of 2-4 heads that share a kv head
 // (head_dim >= 256), two workgroups per CU below head_dim 256.  The ping-pong
 // kernel (head_dim 128, long batches): 8 waves x 32 rows, one workgroup per
 // CU, the two waves of each SIMD kept half a tile apart so one's MFMAs run
-// beside the other's softmax.  K/V tiles of 64 keys are staged in LDS.  Key
+// beside the other's softmax.  The key-halves kernel (short batches): 64
+// query rows, two wave pairs on the two halves of the key range, merged in
+// LDS.  K/V tiles of 64 keys are staged in LDS.  Key
 // tiles outside a wave's visible range are skipped (causal / window), tiles
 // inside every query's range skip the mask.  Workgroups are ordered so each
 // XCD owns whole kv heads (its L2 serves the G query heads that share them)
