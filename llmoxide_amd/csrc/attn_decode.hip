@@ -60,7 +60,7 @@ static long min_tiles_per_wave(int hd) {
     return hd >= 256 ? 1 : 2;
 }
 
-// K row-major through LDS (head_dim 128), or each lane's operand bytes
+// K row-major through LDS (head_dim 128 and 256), or each lane's operand bytes
 // loaded directly.  Rows pay wherever the LDS round trip it adds to a tile is
 // hidden: by other workgroups on the CU (ragged batches: B=8 116 -> 108 us,
 // B=32 358 -> 336 us) or by a short stream (the 512-key C1 decode, 2 tiles a
@@ -68,7 +68,7 @@ static long min_tiles_per_wave(int hd) {
 // (B=1 at 32k) keeps the direct loads, 1% faster there (27.1 against 27.5 us
 // a call).  LMX_DECODE_KROWS=0|1 forces it (read on every call, for tests).
 static bool pick_krows(int hd, int mode, const DecodePlan& pl) {
-    if (hd != 128) return false;
+    if (hd != 128 && hd != 256) return false;
     if (const char* e = std::getenv("LMX_DECODE_KROWS")) return e[0] == '1';
     const int tiles_per_wave = (pl.tps + kWaves / pl.hw - 1) / (kWaves / pl.hw);
     return mode == kModeBatched || pl.n_main > kCusPerGpu || tiles_per_wave <= 4;

@@ -247,11 +247,12 @@ template <typename QT, int HD, int GB, int HW, int MODE, bool KR>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) {
     using Tile = KVTile<HD>;
     constexpr int KS = Tile::KS, VR = Tile::VR, VW = Tile::VW;
-    // KR (head_dim 128): K loaded row-major, as V, and turned into MFMA
-    // operands through LDS, so that each load instruction reads four whole
-    // 256-byte rows instead of 64 bytes of sixteen rows.  The launch picks it
+    // KR (head_dim 128 and 256): K loaded row-major, as V, and turned into
+    // MFMA operands through LDS, so that each load instruction reads four
+    // whole 256-byte row pieces instead of 64 bytes of sixteen rows.  The launch picks it
     // (pick_krows); without it each lane loads its operand bytes directly.
-    constexpr bool KROWS = KR && HD == 128;
+    constexpr bool KROWS = KR && (HD == 128 || HD == 256);
+    constexpr int KRP = HD >= 128 ? HD / 128 : 1;  // 128-dim pieces of a K row (as V's)
     constexpr int DPL = HD / 16;  // V dims per lane
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
@@ -327,11 +328,14 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     auto load_tile = [&](int t, Tile& b) {
         const int kt = lo + kTile * t;
         if constexpr (KROWS) {
-            // K as V: load i, lane (g4, c16) holds key 4 g4 + i, dims
-            // 8 c16 .. + 7 (one 256-byte row per 16 lanes)
+            // K as V: load (i, r), lane (g4, c16) holds key 4 g4 + i, dims
+            // 128 r + 8 c16 .. + 7 (one 256-byte piece per 16 lanes)
 #pragma unroll
-            for (int i = 0; i < KS; ++i)
-                b.k[i] = ld_stream8(row_ptr(kc, a.k_cur, min(kt + 4 * g4 + i, hi)) + 8 * c16);
+            for (int i = 0; i < 4; ++i) {
+                const f16* krow = row_ptr(kc, a.k_cur, min(kt + 4 * g4 + i, hi));
+#pragma unroll
+                for (int r = 0; r < KRP; ++r) b.k[i * KRP + r] = ld_stream8(krow + 128 * r + 8 * c16);
+            }
         } else {
             const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
 #pragma unroll
@@ -479,8 +483,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
                 // Row-major K tile through this wave's LDS slice, read back
                 // as the MFMA A operand (key c16, dims 32 s + 8 g4 .. + 7).
 #pragma unroll
-                for (int i = 0; i < KS; ++i)
-                    *reinterpret_cast<f16x8*>(&K_s[wave][4 * g4 + i][8 * c16]) = b.k[i];
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < KRP; ++r)
+                        *reinterpret_cast<f16x8*>(&K_s[wave][4 * g4 + i][128 * r + 8 * c16]) = b.k[i * KRP + r];
                 wave_lds_sync();
                 f16x8 ka[KS];
 #pragma unroll
@@ -687,7 +693,7 @@ struct DecodePlan {
     int P_ws;          // splits the workspace is sized for (>= P)
     int n_main, n_yg;
     int n_merge, m_parts;
-    bool krows;                // head_dim 128: K row-major through LDS (attn_decode_kernel's KR)
+    bool krows;                // head_dim 128 / 256: K row-major through LDS (attn_decode_kernel's KR)
     size_t ml_bytes, o_bytes;  // what this launch uses
     size_t ws_bytes;           // what the workspace query reports for this shape
     size_t total() const { return ml_bytes + o_bytes; }
@@ -697,7 +703,7 @@ template <typename QT, int MODE, int HW>
 inline lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, bool krows, dim3 grid, hipStream_t st) {
 #define LMX_DEC_CASE(HDV, GBV)                                                                        \
     if (hd == HDV && gb == GBV) {                                                                     \
-        if constexpr (HDV == 128) {                                                                   \
+        if constexpr (HDV == 128 || HDV == 256) {                                                     \
             if (krows) {                                                                              \
                 hipLaunchKernelGGL((attn_decode_kernel<QT, HDV, GBV, HW, MODE, true>), grid,          \
                                    dim3(kDecThreads), 0, st, a);                                      \

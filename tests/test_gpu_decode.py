@@ -188,13 +188,15 @@ def test_one_workspace_serves_every_entry_point():
         assert_close(state.cpu().numpy().ravel(), S_ref, what="delta S")
 
 
-@pytest.mark.parametrize("ctx,window,t,q_f16", [(32768, 0, 1, False), (700, 0, 1, True), (1500, 1024, 1, False),
-                                                 (3000, 0, 4, False)])
-def test_k_operand_paths(ctx, window, t, q_f16, monkeypatch):
-    """Head_dim 128 K tiles both ways, forced: loaded row-major and turned into
-    MFMA operands through LDS, or each lane's operand bytes loaded directly.
-    The operands are the same, so the outputs are the same bits."""
-    c = AttnCase(ctx + t, t=t, H=32, Hkv=8, hd=128, n_pos=ctx, q_f16=q_f16)
+@pytest.mark.parametrize("H,Hkv,hd,ctx,window,t,q_f16", [
+    (32, 8, 128, 32768, 0, 1, False), (32, 8, 128, 700, 0, 1, True), (32, 8, 128, 1500, 1024, 1, False),
+    (32, 8, 128, 3000, 0, 4, False),
+    (16, 8, 256, 1500, 1024, 1, True), (16, 8, 256, 5000, 0, 1, False), (16, 8, 256, 900, 0, 3, True)])
+def test_k_operand_paths(H, Hkv, hd, ctx, window, t, q_f16, monkeypatch):
+    """K tiles both ways (head_dim 128 and 256), forced: loaded row-major and
+    turned into MFMA operands through LDS, or each lane's operand bytes loaded
+    directly.  The operands are the same, so the outputs are the same bits."""
+    c = AttnCase(ctx + t + hd, t=t, H=H, Hkv=Hkv, hd=hd, n_pos=ctx, q_f16=q_f16)
     base = ctx - t
     kc, vc = c.ring(window, ctx) if window else (c.k16, c.v16)
     q = dev(c.q.astype(np.float16)) if q_f16 else dev(c.q)
@@ -204,7 +206,7 @@ def test_k_operand_paths(ctx, window, t, q_f16, monkeypatch):
     for krows in ("0", "1"):
         monkeypatch.setenv("LMX_DECODE_KROWS", krows)
         say(f"K operand path krows={krows} ctx={ctx} w={window} t={t}")
-        out = lmx.attention(q, kd, vd, n_heads=32, n_kv_heads=8, head_dim=128, base_pos=base, window=window)
+        out = lmx.attention(q, kd, vd, n_heads=H, n_kv_heads=Hkv, head_dim=hd, base_pos=base, window=window)
         torch.cuda.synchronize()
         outs.append(out.cpu().numpy())
         assert_close(outs[-1], ref, what=f"krows={krows}")
