@@ -116,6 +116,12 @@ def test_gemm_ragged_edges(name, in_dim, rows, n_tok):
     run(name, rows, in_dim, n_tok, seed=40 + rows + n_tok)
 
 
+@pytest.mark.parametrize("in_dim", [128, 384])
+def test_gemm_one_and_three_chunks(in_dim):
+    # the K loop runs two 128-weight chunks a round: one chunk, and an odd count
+    run("q8_0", 130, in_dim, 70, seed=70 + in_dim)
+
+
 @pytest.mark.parametrize("name", GEMM_TYPES)
 def test_matvec_and_gemm_agree_across_the_threshold(name):
     # 15 tokens take the matvec tiles, 16 the GEMM: both match the oracle
