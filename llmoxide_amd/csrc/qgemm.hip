@@ -21,15 +21,16 @@
 //   |x| must stay below 65504, the f16 range (attention outputs over an f16
 //   V cache always do).
 //
-// Tiles.  A workgroup of four waves owns 64 tokens x 128 weight rows; wave
-// (wm, wn) owns tokens 32 wm .. + 31 and rows 64 wn .. + 63: two 32 x 32
-// MFMA tiles, x as the A operand and q as B, so each lane of a result tile
-// holds one weight row and 16 tokens, and a group's scale is one value per
-// lane.  K goes through LDS 128 weights at a time (half a K-quant
-// super-block, four Q8_0 blocks): x as swizzled f16 hi / lo rows, W decoded
-// to f16 integers with each row's group scales, and the (token, group) x
-// sums.  The next chunk's raw x and W bytes are loaded into registers while
-// the current chunk is multiplied.
+// Tiles.  A workgroup owns 64 tokens x 128 weight rows.  Its four consumer
+// waves multiply: wave (wm, wn) owns tokens 32 wm .. + 31 and rows
+// 64 wn .. + 63, two 32 x 32 MFMA tiles with x as the A operand and q as B,
+// so each lane of a result tile holds one weight row and 16 tokens, and a
+// group's scale is one value per lane.  K goes through LDS 128 weights at a
+// time (half a K-quant super-block, four Q8_0 blocks): x as swizzled f16 hi /
+// lo rows, W decoded to f16 integers with each row's group scales, and the
+// (token, group) x sums.  Its four producer waves load, decode and stash the
+// next chunk into the other of two LDS buffers meanwhile, with the chunk
+// after that already in registers.
 #include "common.hpp"
 
 namespace lmx {
@@ -45,10 +46,8 @@ constexpr int kGM = 64;        // tokens per workgroup
 constexpr int kGN = LMX_QGEMM_ROWS;  // weight rows per workgroup (64 or 128)
 constexpr int kNTW = kGN / 64;       // 32-row MFMA tiles per wave
 constexpr int kGK = 128;       // weights per LDS chunk
-constexpr int kGThreads = 256;
-#ifndef LMX_QGEMM_OCC
-#define LMX_QGEMM_OCC 2  // workgroups per CU the register budget is sized for
-#endif
+constexpr int kGThreads = 512;  // 4 consumer waves (MFMA) + 4 producer waves (loads, decode)
+constexpr int kGHalf = 256;     // threads of each kind
 
 template <int TY>
 struct GTraits;
@@ -222,83 +221,103 @@ __device__ __forceinline__ void stash_w(const uint32_t* rw, int k0, int r, int p
 }
 
 template <int TY>
-__global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
     constexpr int GS = GTraits<TY>::gs;
     constexpr int NG = kGK / GS;          // groups per chunk
     constexpr int KPG = GS / 16;          // MFMA k-steps per group
     constexpr bool OFFSET = TY == kGQ4K;  // groups carry an offset (Q4_K's min)
     constexpr int WW = GTraits<TY>::words;
-    __shared__ __attribute__((aligned(16))) f16 xh_s[kGM * kGK];
-    __shared__ __attribute__((aligned(16))) f16 xl_s[kGM * kGK];
-    __shared__ __attribute__((aligned(16))) f16 q_s[kGN * kGK];
-    __shared__ __attribute__((aligned(16))) f32x2 so_s[kGN * NG];        // (s, o) per row, group
-    __shared__ __attribute__((aligned(16))) float xs_s[OFFSET ? NG * kGM : 4];  // x sums per group, token
+    // Two buffers of every stage: chunk ch lives in buffer ch & 1.
+    __shared__ __attribute__((aligned(16))) f16 xh_s[2][kGM * kGK];
+    __shared__ __attribute__((aligned(16))) f16 xl_s[2][kGM * kGK];
+    __shared__ __attribute__((aligned(16))) f16 q_s[2][kGN * kGK];
+    __shared__ __attribute__((aligned(16))) f32x2 so_s[2][kGN * NG];        // (s, o) per row, group
+    __shared__ __attribute__((aligned(16))) float xs_s[2][OFFSET ? NG * kGM : 4];  // x sums per group, token
 
     const int n_tb = (a.n_tok + kGM - 1) / kGM;
     const int tb = blockIdx.x % n_tb, rb = blockIdx.x / n_tb;
     const int t0 = tb * kGM, r0 = rb * kGN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
+    const int n_chunks = a.in_dim / kGK;
+
+    // Waves 4-7 (producers) load, decode and stash chunk ch + 1 while waves
+    // 0-3 (consumers) multiply chunk ch: a SIMD holds one of each, so the
+    // producer's VALU work issues beside the consumer's MFMAs.  One barrier
+    // per chunk; both kinds of wave execute the same number of barriers.
+    if (tid >= kGHalf) {
+        const int ptid = tid - kGHalf;
+        // ---- register prefetch of one chunk
+        // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
+        // consecutive threads read one token's 512 contiguous bytes.
+        f32x4 rx[8];
+        uint32_t rw[WW];
+        const int w_row = ptid >> 1, w_part = ptid & 1;
+        const bool w_thread = w_row < kGN;  // threads past the tile's rows stage no W
+        const bool w_live = w_thread && r0 + w_row < a.rows;
+        const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
+        auto load_chunk = [&](int k0) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
+                f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                if (t0 + tok < a.n_tok)
+                    v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
+                rx[u] = v;
+            }
+            if (w_thread) load_w<TY>(wrow, k0, w_part, rw);
+        };
+        auto stash_chunk = [&](int k0, int b) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
+                f16x4 hi, lo;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hi[j] = (f16)rx[u][j];
+                    lo[j] = (f16)(rx[u][j] - (float)hi[j]);
+                }
+                const int off = sw(tok, k4 >> 1) + 4 * (k4 & 1);
+                *reinterpret_cast<f16x4*>(&xh_s[b][off]) = hi;
+                *reinterpret_cast<f16x4*>(&xl_s[b][off]) = lo;
+                if constexpr (OFFSET) {
+                    // the group's x sum: eight consecutive lanes hold its 32 floats
+                    float sx = (rx[u][0] + rx[u][1]) + (rx[u][2] + rx[u][3]);
+                    sx += shfl_xor(sx, 1);
+                    sx += shfl_xor(sx, 2);
+                    sx += shfl_xor(sx, 4);
+                    if ((k4 & 7) == 0) xs_s[b][(k4 >> 3) * kGM + tok] = sx;
+                }
+            }
+            if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s[b], so_s[b]);
+        };
+        load_chunk(0);
+        stash_chunk(0, 0);
+        if (n_chunks > 1) load_chunk(kGK);  // in flight during chunk 0's MFMAs
+        __syncthreads();
+        for (int ch = 0; ch < n_chunks; ++ch) {
+            // Buffer (ch + 1) & 1 was last read in iteration ch - 1, before
+            // that iteration's barrier.
+            if (ch + 1 < n_chunks) {
+                stash_chunk((ch + 1) * kGK, (ch + 1) & 1);
+                if (ch + 2 < n_chunks) load_chunk((ch + 2) * kGK);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+
+    const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hh = lane >> 5;
-
-    // ---- register prefetch of one chunk
-    // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
-    // consecutive threads read one token's 512 contiguous bytes.
-    f32x4 rx[8];
-    uint32_t rw[WW];
-    const int w_row = tid >> 1, w_part = tid & 1;
-    const bool w_thread = w_row < kGN;  // threads past the tile's rows stage no W
-    const bool w_live = w_thread && r0 + w_row < a.rows;
-    const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
-    auto load_chunk = [&](int k0) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = tid + kGThreads * u, tok = i >> 5, k4 = i & 31;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (t0 + tok < a.n_tok)
-                v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
-            rx[u] = v;
-        }
-        if (w_thread) load_w<TY>(wrow, k0, w_part, rw);
-    };
-    auto stash_chunk = [&](int k0) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = tid + kGThreads * u, tok = i >> 5, k4 = i & 31;
-            f16x4 hi, lo;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                hi[j] = (f16)rx[u][j];
-                lo[j] = (f16)(rx[u][j] - (float)hi[j]);
-            }
-            const int off = sw(tok, k4 >> 1) + 4 * (k4 & 1);
-            *reinterpret_cast<f16x4*>(&xh_s[off]) = hi;
-            *reinterpret_cast<f16x4*>(&xl_s[off]) = lo;
-            if constexpr (OFFSET) {
-                // the group's x sum: eight consecutive lanes hold its 32 floats
-                float sx = (rx[u][0] + rx[u][1]) + (rx[u][2] + rx[u][3]);
-                sx += shfl_xor(sx, 1);
-                sx += shfl_xor(sx, 2);
-                sx += shfl_xor(sx, 4);
-                if ((k4 & 7) == 0) xs_s[(k4 >> 3) * kGM + tok] = sx;
-            }
-        }
-        if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s, so_s);
-    };
-
     f32x16 y[kNTW];
 #pragma unroll
     for (int n = 0; n < kNTW; ++n)
 #pragma unroll
         for (int j = 0; j < 16; ++j) y[n][j] = 0.f;
 
-    const int n_chunks = a.in_dim / kGK;
-    load_chunk(0);
+    __syncthreads();  // chunk 0 is stashed
     for (int ch = 0; ch < n_chunks; ++ch) {
-        __syncthreads();  // the previous chunk's operand reads are done
-        stash_chunk(ch * kGK);
-        __syncthreads();
-        if (ch + 1 < n_chunks) load_chunk((ch + 1) * kGK);  // in flight during the MFMAs
+        const int b = ch & 1;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             f32x16 acc[kNTW];
@@ -310,13 +329,13 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
             for (int kk = 0; kk < KPG; ++kk) {
                 const int c = 2 * (g * KPG + kk) + hh;
                 const int xr = 32 * wm + l32;
-                const f16x8 ah = *reinterpret_cast<const f16x8*>(&xh_s[sw(xr, c)]);
-                const f16x8 al = *reinterpret_cast<const f16x8*>(&xl_s[sw(xr, c)]);
+                const f16x8 ah = *reinterpret_cast<const f16x8*>(&xh_s[b][sw(xr, c)]);
+                const f16x8 al = *reinterpret_cast<const f16x8*>(&xl_s[b][sw(xr, c)]);
 #pragma unroll
                 for (int n = 0; n < kNTW; ++n) {
-                    const f16x8 b = *reinterpret_cast<const f16x8*>(&q_s[sw(32 * kNTW * wn + 32 * n + l32, c)]);
-                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, acc[n], 0, 0, 0);
-                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, acc[n], 0, 0, 0);
+                    const f16x8 bq = *reinterpret_cast<const f16x8*>(&q_s[b][sw(32 * kNTW * wn + 32 * n + l32, c)]);
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, acc[n], 0, 0, 0);
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, acc[n], 0, 0, 0);
                 }
             }
             // tokens of register j: 8 (j / 4) + 4 hh + j % 4 of the wave's 32
@@ -324,11 +343,11 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
             if constexpr (OFFSET) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4)
-                    xs[q4] = *reinterpret_cast<const f32x4*>(&xs_s[g * kGM + 32 * wm + 8 * q4 + 4 * hh]);
+                    xs[q4] = *reinterpret_cast<const f32x4*>(&xs_s[b][g * kGM + 32 * wm + 8 * q4 + 4 * hh]);
             }
 #pragma unroll
             for (int n = 0; n < kNTW; ++n) {
-                const f32x2 so = so_s[(32 * kNTW * wn + 32 * n + l32) * NG + g];
+                const f32x2 so = so_s[b][(32 * kNTW * wn + 32 * n + l32) * NG + g];
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     float v = fmaf(so[0], acc[n][j], y[n][j]);
@@ -337,6 +356,7 @@ __global__ __launch_bounds__(kGThreads, LMX_QGEMM_OCC) void qgemm_kernel(GemmArg
                 }
             }
         }
+        __syncthreads();  // chunk ch's operands are read; chunk ch + 1 is stashed
     }
 
 #pragma unroll
