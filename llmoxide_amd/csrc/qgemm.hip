@@ -28,9 +28,10 @@
 // group's scale is one value per lane.  K goes through LDS 128 weights at a
 // time (half a K-quant super-block, four Q8_0 blocks): x as swizzled f16 hi /
 // lo rows, W decoded to f16 integers with each row's group scales, and the
-// (token, group) x sums.  Its four producer waves load, decode and stash the
-// next chunk into the other of two LDS buffers meanwhile, with the chunk
-// after that already in registers.
+// (token, group) x sums.  Its producer waves, four for W (load and decode)
+// and four for x (load, hi / lo split and group sums), stash the next chunk
+// into the other of two LDS buffers meanwhile, with the chunk after that
+// already in registers.
 #include "common.hpp"
 
 namespace lmx {
@@ -46,7 +47,7 @@ constexpr int kGM = 64;        // tokens per workgroup
 constexpr int kGN = LMX_QGEMM_ROWS;  // weight rows per workgroup (64 or 128)
 constexpr int kNTW = kGN / 64;       // 32-row MFMA tiles per wave
 constexpr int kGK = 128;       // weights per LDS chunk
-constexpr int kGThreads = 512;  // 4 consumer waves (MFMA) + 4 producer waves (loads, decode)
+constexpr int kGThreads = 768;  // 4 consumer waves (MFMA), 4 W producer waves, 4 x producer waves
 constexpr int kGHalf = 256;     // threads of each kind
 
 template <int TY>
@@ -240,12 +241,14 @@ __global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int n_chunks = a.in_dim / kGK;
 
-    // Waves 4-7 (producers) load, decode and stash chunk ch + 1 while waves
-    // 0-3 (consumers) multiply chunk ch: a SIMD holds one of each, so the
-    // producer's VALU work issues beside the consumer's MFMAs.  One barrier
-    // per chunk; both kinds of wave execute the same number of barriers.
+    // Waves 4-7 (W producers) and 8-11 (x producers) load, decode and stash
+    // chunk ch + 1 while waves 0-3 (consumers) multiply chunk ch: a SIMD
+    // holds one wave of each kind, so the producers' VALU work issues beside
+    // the consumer's MFMAs.  One barrier per chunk; every wave executes the
+    // same number of barriers.
     if (tid >= kGHalf) {
-        const int ptid = tid - kGHalf;
+        const bool x_prod = tid >= 2 * kGHalf;  // wave-uniform
+        const int ptid = tid & (kGHalf - 1);
         // ---- register prefetch of one chunk
         // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
         // consecutive threads read one token's 512 contiguous bytes.
@@ -256,17 +259,24 @@ __global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
         const bool w_live = w_thread && r0 + w_row < a.rows;
         const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
         auto load_chunk = [&](int k0) {
+            if (x_prod) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
-                f32x4 v = {0.f, 0.f, 0.f, 0.f};
-                if (t0 + tok < a.n_tok)
-                    v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
-                rx[u] = v;
+                for (int u = 0; u < 8; ++u) {
+                    const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
+                    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                    if (t0 + tok < a.n_tok)
+                        v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
+                    rx[u] = v;
+                }
+            } else if (w_thread) {
+                load_w<TY>(wrow, k0, w_part, rw);
             }
-            if (w_thread) load_w<TY>(wrow, k0, w_part, rw);
         };
         auto stash_chunk = [&](int k0, int b) {
+            if (!x_prod) {
+                if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s[b], so_s[b]);
+                return;
+            }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
@@ -288,7 +298,6 @@ __global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
                     if ((k4 & 7) == 0) xs_s[b][(k4 >> 3) * kGM + tok] = sx;
                 }
             }
-            if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s[b], so_s[b]);
         };
         load_chunk(0);
         stash_chunk(0, 0);
