@@ -28,8 +28,8 @@
 // group's scale is one value per lane.  K goes through LDS 128 weights at a
 // time (half a K-quant super-block, four Q8_0 blocks): x as swizzled f16 hi /
 // lo rows, W decoded to f16 integers with each row's group scales, and the
-// (token, group) x sums.  Its producer waves, four for W (load and decode)
-// and four for x (load, hi / lo split and group sums), stash the next chunk
+// (token, group) x sums.  Its producer waves, four or eight for W (load and
+// decode) and four for x (load, hi / lo split and group sums), stash the next chunk
 // into the other of two LDS buffers meanwhile, with the chunk after that
 // already in registers.
 #include "common.hpp"
@@ -45,16 +45,27 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #endif
 constexpr int kGM = 64;        // tokens per workgroup
 constexpr int kGN = LMX_QGEMM_ROWS;  // weight rows per workgroup (64 or 128)
-constexpr int kNTW = kGN / 64;       // 32-row MFMA tiles per wave
+#ifndef LMX_QGEMM_CONS
+#define LMX_QGEMM_CONS 4
+#endif
+constexpr int kGCons = LMX_QGEMM_CONS;         // consumer (MFMA) waves: 4 or 8
+constexpr int kNTW = kGN / (16 * kGCons);      // 32-row MFMA tiles per consumer wave
 constexpr int kGK = 128;       // weights per LDS chunk
-constexpr int kGThreads = 768;  // 4 consumer waves (MFMA), 4 W producer waves, 4 x producer waves
-constexpr int kGHalf = 256;     // threads of each kind
+constexpr int kGHalf = 256;                      // x-producer threads
+constexpr int kGConsT = 64 * kGCons;             // consumer threads
+// W-producer threads per row: 4 for Q6_K (one 32-weight unit each: its
+// decode is the heaviest), 2 for Q4_K and Q8_0 (two units each; 4 measured
+// 2% slower for them).
+template <int TY>
+constexpr int g_wparts() { return TY == kGQ6K ? 4 : 2; }
+template <int TY>
+constexpr int g_threads() { return kGConsT + kGN * g_wparts<TY>() + kGHalf; }  // consumers, W, x producers
 
 template <int TY>
 struct GTraits;
 template <> struct GTraits<kGQ4K> { static constexpr int gs = 32, words = 12; };
-template <> struct GTraits<kGQ6K> { static constexpr int gs = 16, words = 15; };
-template <> struct GTraits<kGQ8_0> { static constexpr int gs = 32, words = 18; };
+template <> struct GTraits<kGQ6K> { static constexpr int gs = 16, words = 9; };
+template <> struct GTraits<kGQ8_0> { static constexpr int gs = 32, words = 9; };
 
 struct GemmArgs {
     const uint8_t* w;
@@ -85,23 +96,26 @@ __device__ __forceinline__ float half_bits(uint32_t h) {
 }
 __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xFF; }
 
-// Raw W bytes of one chunk held by thread (row, part); two threads per row.
-//  Q4_K: chunk = half hf of a super-block; part p takes pair 2 hf + p:
+// Raw W bytes of one 32-weight unit (row, part) of a chunk: four units a
+// row, each 32 of the chunk's 128 weights.
+//  Q4_K: chunk = half hf of a super-block; part p is sub-block 4 hf + p, one
+//        nibble (p & 1) of the 32 quant bytes of pair 2 hf + (p >> 1):
 //        words 0-3 the block header (d, dmin, 12 scale bytes), 4-11 the
-//        pair's 32 quant bytes (sub-blocks 2 (2 hf + p) and + 1).
-//  Q6_K: chunk = half h; part p takes l in [16 p, 16 p + 16) of every
-//        32-wide quarter: words 0-3 ql[16 p ..], 4-7 ql[32 + 16 p ..],
-//        8-11 qh[16 p ..] (of the half), 12-13 the half's 8 scales, 14 d.
-//  Q8_0: chunk = four blocks; part p takes blocks 2 p, 2 p + 1 (68 bytes,
-//        as 17 words from a 2-byte aligned start; word 17 unused).
+//        pair's quant bytes.
+//  Q6_K: chunk = half h; part p takes l in [8 p, 8 p + 8) of every 32-wide
+//        quarter: words 0-1 ql[8 p ..], 2-3 ql[32 + 8 p ..], 4-5 qh[8 p ..]
+//        (of the half), 6-7 the half's 8 scales, 8 d.
+//  Q8_0: chunk = four blocks; part p takes block p (34 bytes: words 0-7
+//        bytes 0-31 from a 2-byte aligned start, word 8 bytes 32-33).
 template <int TY>
 __device__ __forceinline__ void load_w(const uint8_t* row, int k0, int part, uint32_t* rw) {
     if constexpr (TY == kGQ4K) {
         const uint8_t* blk = row + (size_t)(k0 >> 8) * 144;
         const int hf = (k0 >> 7) & 1;
         const u32x4 h4 = *reinterpret_cast<const u32x4*>(blk);
-        const u32x4 q0 = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * (2 * hf + part));
-        const u32x4 q1 = *reinterpret_cast<const u32x4*>(blk + 32 + 32 * (2 * hf + part));
+        const uint8_t* qb = blk + 16 + 32 * (2 * hf + (part >> 1));
+        const u32x4 q0 = *reinterpret_cast<const u32x4*>(qb);
+        const u32x4 q1 = *reinterpret_cast<const u32x4*>(qb + 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             rw[i] = h4[i];
@@ -111,24 +125,17 @@ __device__ __forceinline__ void load_w(const uint8_t* row, int k0, int part, uin
     } else if constexpr (TY == kGQ6K) {
         const uint8_t* blk = row + (size_t)(k0 >> 8) * 210;
         const int h = (k0 >> 7) & 1;
-        const uint8_t* ql = blk + 64 * h + 16 * part;
-        const uint8_t* qh = blk + 128 + 32 * h + 16 * part;
+        const uint8_t* ql = blk + 64 * h + 8 * part;
         ld8_a2(ql, rw + 0);
-        ld8_a2(ql + 8, rw + 2);
-        ld8_a2(ql + 32, rw + 4);
-        ld8_a2(ql + 40, rw + 6);
-        ld8_a2(qh, rw + 8);
-        ld8_a2(qh + 8, rw + 10);
-        ld8_a2(blk + 192 + 8 * h, rw + 12);
-        rw[14] = *reinterpret_cast<const uint16_t*>(blk + 208);
+        ld8_a2(ql + 32, rw + 2);
+        ld8_a2(blk + 128 + 32 * h + 8 * part, rw + 4);
+        ld8_a2(blk + 192 + 8 * h, rw + 6);
+        rw[8] = *reinterpret_cast<const uint16_t*>(blk + 208);
     } else {
-        const uint8_t* blk = row + (size_t)((k0 >> 5) + 2 * part) * 34;
+        const uint8_t* blk = row + (size_t)((k0 >> 5) + part) * 34;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ld8_a2(blk + 8 * i, rw + 2 * i);
-        // the last 4 bytes (block 2p+1's final quants) as two 2-byte loads
-        rw[16] = (uint32_t)reinterpret_cast<const uint16_t*>(blk + 64)[0] |
-                 ((uint32_t)reinterpret_cast<const uint16_t*>(blk + 66)[0] << 16);
-        rw[17] = 0u;
+        for (int i = 0; i < 4; ++i) ld8_a2(blk + 8 * i, rw + 2 * i);
+        rw[8] = *reinterpret_cast<const uint16_t*>(blk + 32);
     }
 }
 
@@ -147,82 +154,103 @@ __device__ __forceinline__ void stash_w(const uint32_t* rw, int k0, int r, int p
                                         f32x2* so_s) {
     constexpr int NG = kGK / GTraits<TY>::gs;
     if constexpr (TY == kGQ4K) {
-        // pair p = 2 hf + part: weights 64 part + e; e < 32 low nibble of
-        // quant byte e, else high nibble of byte e - 32 (quant.rs:54-128)
+        // weights 32 part + e of the chunk: nibble (part & 1) of quant byte e
+        // of the pair (quant.rs:54-128)
         const uint32_t* q = rw + 4;
+        const int nib = 4 * (part & 1);
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc) {
+        for (int cc = 0; cc < 4; ++cc) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = (int)((byte_of(q, 8 * cc + j) >> nib) & 0xF);
+            put8(q_s, r, 4 * part + cc, v);
+        }
+        // sub-block j = 4 hf + part: scale and min, quant.rs:33-47
+        const int j = 4 * ((k0 >> 7) & 1) + part;
+        const float d = half_bits(rw[0]), dmin = half_bits(rw[0] >> 16);
+        const uint32_t* sc6 = rw + 1;  // the 12 scale bytes
+        uint32_t sc, m;
+        if (j < 4) {
+            sc = byte_of(sc6, j) & 63;
+            m = byte_of(sc6, j + 4) & 63;
+        } else {
+            sc = (byte_of(sc6, j + 4) & 0xF) | ((byte_of(sc6, j - 4) >> 6) << 4);
+            m = (byte_of(sc6, j + 4) >> 4) | ((byte_of(sc6, j) >> 6) << 4);
+        }
+        so_s[r * NG + part] = live ? f32x2{d * (float)sc, -(dmin * (float)m)} : f32x2{0.f, 0.f};
+    } else if constexpr (TY == kGQ6K) {
+        // weight 32 k + l of the half (l = 8 part + j): low / high nibble
+        // (k >> 1) of ql[l + 32 (k & 1)], with bits 2k, 2k + 1 of qh[l] on
+        // top, minus 32
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
             int v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint32_t b = byte_of(q, 8 * (cc & 3) + j);
-                v[j] = cc < 4 ? (int)(b & 0xF) : (int)(b >> 4);
+                const uint32_t lb = byte_of(rw + 2 * (k & 1), j);
+                const uint32_t hb = byte_of(rw + 4, j);
+                v[j] = (int)(((lb >> (4 * (k >> 1))) & 0xF) | (((hb >> (2 * k)) & 3) << 4)) - 32;
             }
-            put8(q_s, r, 8 * part + cc, v);
+            put8(q_s, r, 4 * k + part, v);
         }
-        // sub-blocks j = 2 (2 hf + part) + {0, 1}: scale and min, quant.rs:33-47
-        const int hf = (k0 >> 7) & 1;
-        const float d = half_bits(rw[0]), dmin = half_bits(rw[0] >> 16);
-        const uint32_t* s = rw + 1;  // the 12 scale bytes
+        // groups of 16: g = 2 k + (l >= 16), written by parts 0 and 2
+        if ((part & 1) == 0) {
+            const float d = half_bits(rw[8]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int j = 2 * (2 * hf + part) + t;
-            uint32_t sc, m;
-            if (j < 4) {
-                sc = byte_of(s, j) & 63;
-                m = byte_of(s, j + 4) & 63;
-            } else {
-                sc = (byte_of(s, j + 4) & 0xF) | ((byte_of(s, j - 4) >> 6) << 4);
-                m = (byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4);
+            for (int k = 0; k < 4; ++k) {
+                const int g = 2 * k + (part >> 1);
+                const float sc = (float)(int8_t)byte_of(rw + 6, g);
+                so_s[r * NG + g] = live ? f32x2{d * sc, 0.f} : f32x2{0.f, 0.f};
             }
-            so_s[r * NG + 2 * part + t] =
-                live ? f32x2{d * (float)sc, -(dmin * (float)m)} : f32x2{0.f, 0.f};
-        }
-    } else if constexpr (TY == kGQ6K) {
-        // weight 32 k + l of the half: low / high nibble (k >> 1) of
-        // ql[l + 32 (k & 1)], with bits 2k, 2k + 1 of qh[l] on top, minus 32
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-#pragma unroll
-            for (int c2 = 0; c2 < 2; ++c2) {
-                int v[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int l = 8 * c2 + j;  // l - 16 part
-                    const uint32_t lb = byte_of(rw + 4 * (k & 1), l);
-                    const uint32_t hb = byte_of(rw + 8, l);
-                    v[j] = (int)(((lb >> (4 * (k >> 1))) & 0xF) | (((hb >> (2 * k)) & 3) << 4)) - 32;
-                }
-                put8(q_s, r, 4 * k + 2 * part + c2, v);
-            }
-        }
-        const float d = half_bits(rw[14]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int g = 2 * k + part;
-            const float sc = (float)(int8_t)byte_of(rw + 12, g);
-            so_s[r * NG + g] = live ? f32x2{d * sc, 0.f} : f32x2{0.f, 0.f};
         }
     } else {
-        // block b = 2 part + bi: d at bytes 34 bi, quants at 34 bi + 2
+        // block part: d at bytes 0-1, quants at bytes 2-33
+        const float d = half_bits(byte_of(rw, 0) | (byte_of(rw, 1) << 8));
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            const int base = 34 * bi;
-            const float d = half_bits(byte_of(rw, base) | (byte_of(rw, base + 1) << 8));
+        for (int cc = 0; cc < 4; ++cc) {
+            int v[8];
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                int v[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = (int)(int8_t)byte_of(rw, base + 2 + 8 * cc + j);
-                put8(q_s, r, 4 * (2 * part + bi) + cc, v);
-            }
-            so_s[r * NG + 2 * part + bi] = live ? f32x2{d, 0.f} : f32x2{0.f, 0.f};
+            for (int j = 0; j < 8; ++j) v[j] = (int)(int8_t)byte_of(rw, 2 + 8 * cc + j);
+            put8(q_s, r, 4 * part + cc, v);
         }
+        so_s[r * NG + part] = live ? f32x2{d, 0.f} : f32x2{0.f, 0.f};
+    }
+}
+
+// Q8_0, two units a thread: blocks 2 pair and 2 pair + 1 of the chunk, 68
+// contiguous bytes (dword-aligned when rows are, as 4096-wide ones are) as
+// 17 words; separate 34-byte units would put every other block 2 bytes off a
+// dword (15-20% slower).
+__device__ __forceinline__ void load_q8_pair(const uint8_t* row, int k0, int pair, uint32_t* rw) {
+    const uint8_t* blk = row + (size_t)((k0 >> 5) + 2 * pair) * 34;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ld8_a2(blk + 8 * i, rw + 2 * i);
+    // the last 4 bytes (block 2 pair + 1's final quants) as two 2-byte loads
+    rw[16] = (uint32_t)reinterpret_cast<const uint16_t*>(blk + 64)[0] |
+             ((uint32_t)reinterpret_cast<const uint16_t*>(blk + 66)[0] << 16);
+    rw[17] = 0u;
+}
+__device__ __forceinline__ void stash_q8_pair(const uint32_t* rw, int r, int pair, bool live, f16* q_s,
+                                              f32x2* so_s) {
+    constexpr int NG = kGK / GTraits<kGQ8_0>::gs;
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+        // block 2 pair + bi: d at bytes 34 bi, quants at 34 bi + 2
+        const int base = 34 * bi;
+        const float d = half_bits(byte_of(rw, base) | (byte_of(rw, base + 1) << 8));
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = (int)(int8_t)byte_of(rw, base + 2 + 8 * cc + j);
+            put8(q_s, r, 4 * (2 * pair + bi) + cc, v);
+        }
+        so_s[r * NG + 2 * pair + bi] = live ? f32x2{d, 0.f} : f32x2{0.f, 0.f};
     }
 }
 
 template <int TY>
-__global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
     constexpr int GS = GTraits<TY>::gs;
     constexpr int NG = kGK / GS;          // groups per chunk
     constexpr int KPG = GS / 16;          // MFMA k-steps per group
@@ -241,20 +269,24 @@ __global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int n_chunks = a.in_dim / kGK;
 
-    // Waves 4-7 (W producers) and 8-11 (x producers) load, decode and stash
-    // chunk ch + 1 while waves 0-3 (consumers) multiply chunk ch: a SIMD
-    // holds one wave of each kind, so the producers' VALU work issues beside
-    // the consumer's MFMAs.  One barrier per chunk; every wave executes the
-    // same number of barriers.
-    if (tid >= kGHalf) {
-        const bool x_prod = tid >= 2 * kGHalf;  // wave-uniform
-        const int ptid = tid & (kGHalf - 1);
+    // The W-producer waves (eight for Q6_K, else four) and x-producer waves
+    // (four) load, decode and stash chunk ch + 1 while the consumer waves (the
+    // first kGCons) multiply chunk
+    // ch: a SIMD holds waves of every kind, so the producers' VALU work issues
+    // beside the consumers' MFMAs.  One barrier per chunk; every wave executes
+    // the same number of barriers.
+    constexpr int WPARTS = g_wparts<TY>(), WU = 4 / WPARTS;  // threads a row, units a thread
+    constexpr int WT = kGN * WPARTS;                           // W-producer threads
+    if (tid >= kGConsT) {
+        const bool x_prod = tid >= kGConsT + WT;  // wave-uniform
+        const int ptid = x_prod ? tid - kGConsT - WT : tid - kGConsT;
         // ---- register prefetch of one chunk
         // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
         // consecutive threads read one token's 512 contiguous bytes.
         f32x4 rx[8];
-        uint32_t rw[WW];
-        const int w_row = ptid >> 1, w_part = ptid & 1;
+        constexpr bool Q8PAIR = TY == kGQ8_0 && WU == 2;
+        uint32_t rw[WU][Q8PAIR ? 18 : WW];
+        const int w_row = ptid / WPARTS, w_part = ptid % WPARTS;
         const bool w_thread = w_row < kGN;  // threads past the tile's rows stage no W
         const bool w_live = w_thread && r0 + w_row < a.rows;
         const uint8_t* wrow = a.w + (size_t)(w_live ? r0 + w_row : 0) * a.row_bytes;
@@ -269,12 +301,25 @@ __global__ __launch_bounds__(kGThreads, 1) void qgemm_kernel(GemmArgs a) {
                     rx[u] = v;
                 }
             } else if (w_thread) {
-                load_w<TY>(wrow, k0, w_part, rw);
+                if constexpr (Q8PAIR) {
+                    load_q8_pair(wrow, k0, w_part, rw[0]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < WU; ++u) load_w<TY>(wrow, k0, w_part * WU + u, rw[u]);
+                }
             }
         };
         auto stash_chunk = [&](int k0, int b) {
             if (!x_prod) {
-                if (w_thread) stash_w<TY>(rw, k0, w_row, w_part, w_live, q_s[b], so_s[b]);
+                if (w_thread) {
+                    if constexpr (Q8PAIR) {
+                        stash_q8_pair(rw[0], w_row, w_part, w_live, q_s[b], so_s[b]);
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < WU; ++u)
+                            stash_w<TY>(rw[u], k0, w_row, w_part * WU + u, w_live, q_s[b], so_s[b]);
+                    }
+                }
                 return;
             }
 #pragma unroll
@@ -405,9 +450,9 @@ lmx_status qgemm(const lmx_qmv_desc* d, const void* w, const float* x, float* y,
     const dim3 grid((unsigned)(n_tb * n_rb));
     (void)hipGetLastError();
     switch (d->type) {
-        case kGQ4K: hipLaunchKernelGGL(qgemm_kernel<kGQ4K>, grid, dim3(kGThreads), 0, st, a); break;
-        case kGQ6K: hipLaunchKernelGGL(qgemm_kernel<kGQ6K>, grid, dim3(kGThreads), 0, st, a); break;
-        default: hipLaunchKernelGGL(qgemm_kernel<kGQ8_0>, grid, dim3(kGThreads), 0, st, a); break;
+        case kGQ4K: hipLaunchKernelGGL(qgemm_kernel<kGQ4K>, grid, dim3(g_threads<kGQ4K>()), 0, st, a); break;
+        case kGQ6K: hipLaunchKernelGGL(qgemm_kernel<kGQ6K>, grid, dim3(g_threads<kGQ6K>()), 0, st, a); break;
+        default: hipLaunchKernelGGL(qgemm_kernel<kGQ8_0>, grid, dim3(g_threads<kGQ8_0>()), 0, st, a); break;
     }
     LMX_CHECK_LAUNCH();
     return LMX_OK;
