@@ -51,15 +51,20 @@ constexpr int kGN = LMX_QGEMM_ROWS;  // weight rows per workgroup (64 or 128)
 constexpr int kGCons = LMX_QGEMM_CONS;         // consumer (MFMA) waves: 4 or 8
 constexpr int kNTW = kGN / (16 * kGCons);      // 32-row MFMA tiles per consumer wave
 constexpr int kGK = 128;       // weights per LDS chunk
-constexpr int kGHalf = 256;                      // x-producer threads
+constexpr int kGXF = 2048;                       // float4s of x in a chunk (64 tokens x 128)
 constexpr int kGConsT = 64 * kGCons;             // consumer threads
 // W-producer threads per row: 4 for Q6_K (one 32-weight unit each: its
 // decode is the heaviest), 2 for Q4_K and Q8_0 (two units each; 4 measured
 // 2% slower for them).
 template <int TY>
 constexpr int g_wparts() { return TY == kGQ6K ? 4 : 2; }
+// x-producer threads: 512 (four float4s of a chunk each) for Q4_K, whose x
+// producers also form the group sums (73 -> 63.5 us against 256), 256 (eight
+// each) for Q8_0 (512 measured 5% slower) and Q6_K (eight W waves).
 template <int TY>
-constexpr int g_threads() { return kGConsT + kGN * g_wparts<TY>() + kGHalf; }  // consumers, W, x producers
+constexpr int g_xthreads() { return TY == kGQ4K ? 512 : 256; }
+template <int TY>
+constexpr int g_threads() { return kGConsT + kGN * g_wparts<TY>() + g_xthreads<TY>(); }  // consumers, W, x producers
 
 template <int TY>
 struct GTraits;
@@ -281,9 +286,10 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
         const bool x_prod = tid >= kGConsT + WT;  // wave-uniform
         const int ptid = x_prod ? tid - kGConsT - WT : tid - kGConsT;
         // ---- register prefetch of one chunk
-        // x: 64 tokens x 128 floats = 2048 float4, eight per thread; 32
+        // x: 64 tokens x 128 floats = 2048 float4, XU per thread; 32
         // consecutive threads read one token's 512 contiguous bytes.
-        f32x4 rx[8];
+        constexpr int XT = g_xthreads<TY>(), XU = kGXF / XT;  // x-producer threads, float4s a thread
+        f32x4 rx[XU];
         constexpr bool Q8PAIR = TY == kGQ8_0 && WU == 2;
         uint32_t rw[WU][Q8PAIR ? 18 : WW];
         const int w_row = ptid / WPARTS, w_part = ptid % WPARTS;
@@ -293,8 +299,8 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
         auto load_chunk = [&](int k0) {
             if (x_prod) {
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
+                for (int u = 0; u < XU; ++u) {
+                    const int i = ptid + XT * u, tok = i >> 5, k4 = i & 31;
                     f32x4 v = {0.f, 0.f, 0.f, 0.f};
                     if (t0 + tok < a.n_tok)
                         v = *reinterpret_cast<const f32x4*>(a.x + (size_t)(t0 + tok) * a.in_dim + k0 + 4 * k4);
@@ -323,8 +329,8 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
                 return;
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int i = ptid + kGHalf * u, tok = i >> 5, k4 = i & 31;
+            for (int u = 0; u < XU; ++u) {
+                const int i = ptid + XT * u, tok = i >> 5, k4 = i & 31;
                 f16x4 hi, lo;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
