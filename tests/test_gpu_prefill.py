@@ -102,15 +102,13 @@ def test_prefill_head_geometries(H, Hkv, hd):
     check(c, base=50, scale=1.0 / np.sqrt(hd))
 
 
-@pytest.mark.parametrize("gp", [1, 2, 4])
-@pytest.mark.parametrize("H,Hkv,hd,window", [(16, 4, 128, 0), (16, 4, 128, 150), (8, 2, 256, 0),
-                                             (16, 8, 256, 300)])
+@pytest.mark.parametrize("gp,H,Hkv,hd,window", [
+    (gp, H, Hkv, hd, w) for (H, Hkv, hd, w) in [(16, 4, 128, 0), (16, 4, 128, 150), (8, 2, 256, 0), (16, 8, 256, 300)]
+    for gp in (1, 2, 4) if (H // Hkv) % gp == 0])
 def test_prefill_heads_per_workgroup(gp, H, Hkv, hd, window, monkeypatch):
     """Query heads of one kv group packed into a workgroup (128 / gp rows
     each): ragged t, a window, and a ring with k_cur rows, against the oracle.
-    gp = 4 only where it divides G."""
-    if (H // Hkv) % gp:
-        pytest.skip("gp must divide the group size")
+    gp takes every value in {1, 2, 4} that divides the group size."""
     monkeypatch.setenv("LMX_PREFILL_GP", str(gp))
     c = AttnCase(gp * 1000 + H + hd + window, t=333, H=H, Hkv=Hkv, hd=hd, n_pos=333 + 400, q_f16=True)
     say(f"heads per workgroup gp={gp}")
