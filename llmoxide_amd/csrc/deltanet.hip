@@ -261,7 +261,7 @@ struct ChunkSmem {
 // (K and Q rows for X and Y, K^T for the state update) to ws_K, so the 16
 // scan workgroups that read a k-head's chunk split nothing themselves.
 template <int SD, int C, bool SPLIT>
-__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
+__global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
                                                                float* ws_P, float* ws_e,
                                                                uint8_t* ws_K, int n_chunks) {
     constexpr int NM = C / 16, LD = ChunkSmem<C>::LD;
@@ -277,239 +277,263 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(DeltaArgs a, floa
     float* const Ps = smem + 2 * C * LD;  // P
     __shared__ __attribute__((aligned(16))) float lg_w[4][64];  // one copy per wave
     __shared__ __attribute__((aligned(16))) float b_w[4][64];
-    const int ch = blockIdx.x, hk = blockIdx.y, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c0 = ch * C, nv = min(C, a.n_tok - c0);
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-    // alpha and beta of the next v-head, in flight during the work before it
-    float al_n = 0.f, be_n = 0.f;
-    auto ab_fetch = [&](int hv) {
-        if (lane < nv) {
-            const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
-            al_n = a.alpha[gi];
-            be_n = a.beta[gi];
+    // Items (chunk, k-head) blockIdx.x, + gridDim.x, ... (two workgroups a
+    // CU): the next item's K and Q rows load into registers while this one is
+    // worked, so only a workgroup's first staging waits on memory (staging
+    // was a third of a workgroup's time, all of them loading at once).
+    // Rows past the end of the batch are zero.
+    constexpr int SJ = C * SD / 4 / 256;
+    f32x4 rq[SJ], rk[SJ];
+    const int n_items = n_chunks * a.n_kh;
+    auto load_rows = [&](int item) {
+        const int lc0 = (item % n_chunks) * C, lnv = min(C, a.n_tok - lc0), lhk = item / n_chunks;
+#pragma unroll
+        for (int j = 0; j < SJ; ++j) {
+            const int idx = tid + 256 * j, row = idx / (SD / 4), c4 = idx % (SD / 4);
+            f32x4 q = z4, k = z4;
+            if (row < lnv) {
+                const float* src = a.conv + (size_t)(lc0 + row) * a.conv_dim + (size_t)lhk * SD + 4 * c4;
+                q = ld4(src);
+                k = ld4(src + a.key_dim);
+            }
+            rq[j] = q;
+            rk[j] = k;
         }
     };
-    ab_fetch(hk);
+    if ((int)blockIdx.x < n_items) load_rows(blockIdx.x);
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int ch = item % n_chunks, hk = item / n_chunks;
+        const int c0 = ch * C, nv = min(C, a.n_tok - c0);
 
-    // Stage the chunk's K and Q rows; rows past the end are zero.
-#pragma unroll
-    for (int j = 0; j < C * SD / 4 / 256; ++j) {
-        const int idx = tid + 256 * j, row = idx / (SD / 4), c4 = idx % (SD / 4);
-        f32x4 q = z4, k = z4;
-        if (row < nv) {
-            const float* src = a.conv + (size_t)(c0 + row) * a.conv_dim + (size_t)hk * SD + 4 * c4;
-            q = ld4(src);
-            k = ld4(src + a.key_dim);
-        }
-        *reinterpret_cast<f32x4*>(Qs + row * KLD + 4 * c4) = q;
-        *reinterpret_cast<f32x4*>(Ks + row * KLD + 4 * c4) = k;
-    }
-    __syncthreads();
-
-    // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
-    // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
-    f32x4 gk[TPW], gq[TPW];
-    int tile_m[TPW], tile_n[TPW];
-#pragma unroll
-    for (int k = 0; k < TPW; ++k) {
-        int m = 0, n = w + 4 * k;
-        while (n > m) {
-            n -= m + 1;
-            ++m;
-        }
-        tile_m[k] = m;
-        tile_n[k] = n;
-        gk[k] = z4;
-        gq[k] = z4;
-        if (w + 4 * k >= NTILE) continue;
-        const float* km = Ks + (16 * m + lr) * KLD + 4 * lq;
-        const float* qm = Qs + (16 * m + lr) * KLD + 4 * lq;
-        const float* kn = Ks + (16 * n + lr) * KLD + 4 * lq;
-#pragma unroll
-        for (int u = 0; u < SD / 16; ++u) {
-            const f32x4 a4 = ld4(km + 16 * u), q4 = ld4(qm + 16 * u), b4 = ld4(kn + 16 * u);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                gk[k] = mfma4(a4[r], b4[r], gk[k]);
-                gq[k] = mfma4(q4[r], b4[r], gq[k]);
-            }
-        }
-    }
-
-    if constexpr (SPLIT) {
-        // K, Q pieces (token tile m, dim step sg): lane (lr, lq) row 16 m + lr,
-        // dims 32 sg + 4 lq + {0..3} and + 16.  K^T pieces (dim tile ct, token
-        // step sg): lane (lr, lq) dim 16 ct + lr, tokens 32 sg + 4 lq + {0..3}
-        // and + 16.  Staged rows past the chunk's end are zero.
-        constexpr int SX = SD / 32, SC = C / 32;
-        uint8_t* kb = ws_K + ((size_t)ch * a.n_kh + hk) * (3 * C * SD * 4);
-        for (int q = tid; q < NM * SX * 64; q += 256) {
-            const int l = q & 63, pc = q >> 6, m = pc / SX, sg = pc % SX;
-            const int t = 16 * m + (l & 15), c0 = 32 * sg + 4 * (l >> 4);
-            st_piece(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)));
-            st_piece(kb + C * SD * 4 + pc * kPiece, l,
-                     split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)));
-        }
-        for (int q = tid; q < (SD / 16) * SC * 64; q += 256) {
-            const int l = q & 63, pc = q >> 6, ct = pc / SC, sg = pc % SC;
-            const int d = 16 * ct + (l & 15), t0 = 32 * sg + 4 * (l >> 4);
-            f32x4 x0, x1;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                x0[r] = Ks[(t0 + r) * KLD + d];
-                x1[r] = Ks[(t0 + 16 + r) * KLD + d];
-            }
-            st_piece(kb + 2 * C * SD * 4 + pc * kPiece, l, split8(x0, x1));
-        }
-    }
-
-    for (int hv = hk; hv < a.n_vh; hv += a.n_kh) {
-        const size_t cb = (size_t)hv * n_chunks + ch;
-        // the staging (first head) or the previous head's A, T, P are no longer read
-        __syncthreads();
-        // Every wave forms the log2-decay cumsum and b for lane = token itself.
-        {
-            float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
+        // alpha and beta of the next v-head, in flight during the work before it
+        float al_n = 0.f, be_n = 0.f;
+        auto ab_fetch = [&](int hv) {
             if (lane < nv) {
-                l = kLog2e * a.ssm_a[hv] * softplus_f(al_n + a.dt_bias[hv]);
-                b = 1.f / (1.f + expf(-be_n));
+                const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
+                al_n = a.alpha[gi];
+                be_n = a.beta[gi];
             }
-            if (hv + a.n_kh < a.n_vh) ab_fetch(hv + a.n_kh);
+        };
+        ab_fetch(hk);
+
+        // Stage the chunk's K and Q rows (the previous item's LDS reads are done).
+        __syncthreads();
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(l, off);
-                if (lane >= off) l += y;
-            }
-            lg_w[w][lane] = l;
-            b_w[w][lane] = b;
-            if (w == 0 && lane < C) {
-                const float lgC = __shfl(l, C - 1);
-                ws_e[cb * 2 * C + lane] = fast_exp2(l);
-                ws_e[cb * 2 * C + C + lane] = fast_exp2(lgC - l);
-            }
+        for (int j = 0; j < SJ; ++j) {
+            const int idx = tid + 256 * j, row = idx / (SD / 4), c4 = idx % (SD / 4);
+            *reinterpret_cast<f32x4*>(Qs + row * KLD + 4 * c4) = rq[j];
+            *reinterpret_cast<f32x4*>(Ks + row * KLD + 4 * c4) = rk[j];
         }
-        __builtin_amdgcn_wave_barrier();
+        __syncthreads();
+        if (item + (int)gridDim.x < n_items) load_rows(item + gridDim.x);
+
+        // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
+        // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
+        f32x4 gk[TPW], gq[TPW];
+        int tile_m[TPW], tile_n[TPW];
 #pragma unroll
         for (int k = 0; k < TPW; ++k) {
+            int m = 0, n = w + 4 * k;
+            while (n > m) {
+                n -= m + 1;
+                ++m;
+            }
+            tile_m[k] = m;
+            tile_n[k] = n;
+            gk[k] = z4;
+            gq[k] = z4;
             if (w + 4 * k >= NTILE) continue;
-            const int i = 16 * tile_n[k] + lr;
-            const float li = lg_w[w][i];
+            const float* km = Ks + (16 * m + lr) * KLD + 4 * lq;
+            const float* qm = Qs + (16 * m + lr) * KLD + 4 * lq;
+            const float* kn = Ks + (16 * n + lr) * KLD + 4 * lq;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * tile_m[k] + 4 * lq + r;
-                const float dec = i <= t ? fast_exp2(lg_w[w][t] - li) : 0.f;
-                As[t * LD + i] = i < t ? b_w[w][t] * dec * gk[k][r] : 0.f;
-                Ps[t * LD + i] = dec * gq[k][r];
+            for (int u = 0; u < SD / 16; ++u) {
+                const f32x4 a4 = ld4(km + 16 * u), q4 = ld4(qm + 16 * u), b4 = ld4(kn + 16 * u);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    gk[k] = mfma4(a4[r], b4[r], gk[k]);
+                    gq[k] = mfma4(q4[r], b4[r], gq[k]);
+                }
             }
         }
-        __syncthreads();  // A and P complete
 
-        // (I + A)^-1 by 16x16 blocks.  Diagonal blocks by forward substitution,
-        // lane lr owning column lr of block w:
-        //   T[t][c] = [t == c] - sum_{i < t} A[t][i] T[i][c]
-        if (w < NM) {
-            const int base = 16 * w;
-            float tv[16];
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                float s = t == lr ? 1.f : 0.f;
-                const float* arow = As + (base + t) * LD + base;
-#pragma unroll
-                for (int i = 0; i < t; ++i) s = fmaf(-arow[i], tv[i], s);
-                tv[t] = s;
+        if constexpr (SPLIT) {
+            // K, Q pieces (token tile m, dim step sg): lane (lr, lq) row 16 m + lr,
+            // dims 32 sg + 4 lq + {0..3} and + 16.  K^T pieces (dim tile ct, token
+            // step sg): lane (lr, lq) dim 16 ct + lr, tokens 32 sg + 4 lq + {0..3}
+            // and + 16.  Staged rows past the chunk's end are zero.
+            constexpr int SX = SD / 32, SC = C / 32;
+            uint8_t* kb = ws_K + ((size_t)ch * a.n_kh + hk) * (3 * C * SD * 4);
+            for (int q = tid; q < NM * SX * 64; q += 256) {
+                const int l = q & 63, pc = q >> 6, m = pc / SX, sg = pc % SX;
+                const int t = 16 * m + (l & 15), c0 = 32 * sg + 4 * (l >> 4);
+                st_piece(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)));
+                st_piece(kb + C * SD * 4 + pc * kPiece, l,
+                         split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)));
             }
-            if (lq == 0)
+            for (int q = tid; q < (SD / 16) * SC * 64; q += 256) {
+                const int l = q & 63, pc = q >> 6, ct = pc / SC, sg = pc % SC;
+                const int d = 16 * ct + (l & 15), t0 = 32 * sg + 4 * (l >> 4);
+                f32x4 x0, x1;
 #pragma unroll
-                for (int t = 0; t < 16; ++t) Tm[(base + t) * LD + base + lr] = tv[t];
+                for (int r = 0; r < 4; ++r) {
+                    x0[r] = Ks[(t0 + r) * KLD + d];
+                    x1[r] = Ks[(t0 + 16 + r) * KLD + d];
+                }
+                st_piece(kb + 2 * C * SD * 4 + pc * kPiece, l, split8(x0, x1));
+            }
         }
-        // Off-diagonal blocks level by level:
-        //   T[M][N] = -T[M][M] * sum_{N <= Q < M} A[M][Q] T[Q][N]
-        for (int lev = 1; lev < NM; ++lev) {
+
+        for (int hv = hk; hv < a.n_vh; hv += a.n_kh) {
+            const size_t cb = (size_t)hv * n_chunks + ch;
+            // the staging (first head) or the previous head's A, T, P are no longer read
             __syncthreads();
-            if (w < NM - lev) {
-                const int N = w, M = w + lev;
-                f32x4 x = z4;
-                for (int Q = N; Q < M; ++Q) {
-                    const f32x4 av = ld4(As + (16 * M + lr) * LD + 16 * Q + 4 * lq);
+            // Every wave forms the log2-decay cumsum and b for lane = token itself.
+            {
+                float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
+                if (lane < nv) {
+                    l = kLog2e * a.ssm_a[hv] * softplus_f(al_n + a.dt_bias[hv]);
+                    b = 1.f / (1.f + expf(-be_n));
+                }
+                if (hv + a.n_kh < a.n_vh) ab_fetch(hv + a.n_kh);
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const float y = __shfl_up(l, off);
+                    if (lane >= off) l += y;
+                }
+                lg_w[w][lane] = l;
+                b_w[w][lane] = b;
+                if (w == 0 && lane < C) {
+                    const float lgC = __shfl(l, C - 1);
+                    ws_e[cb * 2 * C + lane] = fast_exp2(l);
+                    ws_e[cb * 2 * C + C + lane] = fast_exp2(lgC - l);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+                if (w + 4 * k >= NTILE) continue;
+                const int i = 16 * tile_n[k] + lr;
+                const float li = lg_w[w][i];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tile_m[k] + 4 * lq + r;
+                    const float dec = i <= t ? fast_exp2(lg_w[w][t] - li) : 0.f;
+                    As[t * LD + i] = i < t ? b_w[w][t] * dec * gk[k][r] : 0.f;
+                    Ps[t * LD + i] = dec * gq[k][r];
+                }
+            }
+            __syncthreads();  // A and P complete
+
+            // (I + A)^-1 by 16x16 blocks.  Diagonal blocks by forward substitution,
+            // lane lr owning column lr of block w:
+            //   T[t][c] = [t == c] - sum_{i < t} A[t][i] T[i][c]
+            if (w < NM) {
+                const int base = 16 * w;
+                float tv[16];
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    float s = t == lr ? 1.f : 0.f;
+                    const float* arow = As + (base + t) * LD + base;
+#pragma unroll
+                    for (int i = 0; i < t; ++i) s = fmaf(-arow[i], tv[i], s);
+                    tv[t] = s;
+                }
+                if (lq == 0)
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) Tm[(base + t) * LD + base + lr] = tv[t];
+            }
+            // Off-diagonal blocks level by level:
+            //   T[M][N] = -T[M][M] * sum_{N <= Q < M} A[M][Q] T[Q][N]
+            for (int lev = 1; lev < NM; ++lev) {
+                __syncthreads();
+                if (w < NM - lev) {
+                    const int N = w, M = w + lev;
+                    f32x4 x = z4;
+                    for (int Q = N; Q < M; ++Q) {
+                        const f32x4 av = ld4(As + (16 * M + lr) * LD + 16 * Q + 4 * lq);
+#pragma unroll
+                        for (int s = 0; s < 4; ++s)
+                            x = mfma4(av[s], Tm[(16 * Q + 4 * lq + s) * LD + 16 * N + lr], x);
+                    }
+                    const f32x4 tv = ld4(Tm + (16 * M + lr) * LD + 16 * M + 4 * lq);
+                    f32x4 y = z4;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) y = mfma4(tv[s], x[s], y);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) Tm[(16 * M + 4 * lq + r) * LD + 16 * N + lr] = -y[r];
+                }
+            }
+            __syncthreads();
+            // M = P Tb on the blocks at or below the diagonal, into As (free now):
+            //   M[m][n] = sum_{n <= k <= m} P[m][k] T[k][n] diag(b)
+#pragma unroll
+            for (int q = 0; q < TPW; ++q) {
+                if (w + 4 * q >= NTILE) continue;
+                const int m = tile_m[q], n = tile_n[q];
+                const float bc = b_w[w][16 * n + lr];
+                f32x4 acc = z4;
+                for (int k = n; k <= m; ++k) {
+                    const f32x4 pv = ld4(Ps + (16 * m + lr) * LD + 16 * k + 4 * lq);
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
-                        x = mfma4(av[s], Tm[(16 * Q + 4 * lq + s) * LD + 16 * N + lr], x);
+                        acc = mfma4(pv[s], Tm[(16 * k + 4 * lq + s) * LD + 16 * n + lr] * bc, acc);
                 }
-                const f32x4 tv = ld4(Tm + (16 * M + lr) * LD + 16 * M + 4 * lq);
-                f32x4 y = z4;
 #pragma unroll
-                for (int s = 0; s < 4; ++s) y = mfma4(tv[s], x[s], y);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) Tm[(16 * M + 4 * lq + r) * LD + 16 * N + lr] = -y[r];
+                for (int r = 0; r < 4; ++r) As[(16 * m + 4 * lq + r) * LD + 16 * n + lr] = acc[r];
             }
-        }
-        __syncthreads();
-        // M = P Tb on the blocks at or below the diagonal, into As (free now):
-        //   M[m][n] = sum_{n <= k <= m} P[m][k] T[k][n] diag(b)
+            __syncthreads();
+            if constexpr (SPLIT) {
+                // Tb and M as split pieces (row tile bm, token step sg): lane
+                // (lr, lq) row 16 bm + lr, columns 32 sg + 4 lq + {0..3} and + 16.
+                // Entries above the diagonal (Tb) or in blocks above it (M) are 0.
+                constexpr int SC = C / 32;
+                uint8_t* Tg = reinterpret_cast<uint8_t*>(ws_T + cb * C * C);
+                uint8_t* Mg = reinterpret_cast<uint8_t*>(ws_P + cb * C * C);
+                for (int q = tid; q < NM * SC * 64; q += 256) {
+                    const int l = q & 63, pc = q >> 6, bm = pc / SC, sg = pc % SC;
+                    const int t = 16 * bm + (l & 15);
+                    f32x4 to[2], mo[2];
 #pragma unroll
-        for (int q = 0; q < TPW; ++q) {
-            if (w + 4 * q >= NTILE) continue;
-            const int m = tile_m[q], n = tile_n[q];
-            const float bc = b_w[w][16 * n + lr];
-            f32x4 acc = z4;
-            for (int k = n; k <= m; ++k) {
-                const f32x4 pv = ld4(Ps + (16 * m + lr) * LD + 16 * k + 4 * lq);
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const int i0 = 32 * sg + 16 * hf + 4 * (l >> 4), bn = 2 * sg + hf;
+                        const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    acc = mfma4(pv[s], Tm[(16 * k + 4 * lq + s) * LD + 16 * n + lr] * bc, acc);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) As[(16 * m + 4 * lq + r) * LD + 16 * n + lr] = acc[r];
-        }
-        __syncthreads();
-        if constexpr (SPLIT) {
-            // Tb and M as split pieces (row tile bm, token step sg): lane
-            // (lr, lq) row 16 bm + lr, columns 32 sg + 4 lq + {0..3} and + 16.
-            // Entries above the diagonal (Tb) or in blocks above it (M) are 0.
-            constexpr int SC = C / 32;
-            uint8_t* Tg = reinterpret_cast<uint8_t*>(ws_T + cb * C * C);
-            uint8_t* Mg = reinterpret_cast<uint8_t*>(ws_P + cb * C * C);
-            for (int q = tid; q < NM * SC * 64; q += 256) {
-                const int l = q & 63, pc = q >> 6, bm = pc / SC, sg = pc % SC;
-                const int t = 16 * bm + (l & 15);
-                f32x4 to[2], mo[2];
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const int i0 = 32 * sg + 16 * hf + 4 * (l >> 4), bn = 2 * sg + hf;
-                    const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        to[hf][e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
-                        mo[hf][e] = bn <= bm ? mv[e] : 0.f;
+                        for (int e = 0; e < 4; ++e) {
+                            to[hf][e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
+                            mo[hf][e] = bn <= bm ? mv[e] : 0.f;
+                        }
                     }
+                    st_piece(Tg + pc * kPiece, l, split8(to[0], to[1]));
+                    st_piece(Mg + pc * kPiece, l, split8(mo[0], mo[1]));
                 }
-                st_piece(Tg + pc * kPiece, l, split8(to[0], to[1]));
-                st_piece(Mg + pc * kPiece, l, split8(mo[0], mo[1]));
+                continue;
             }
-            continue;
-        }
-        // Tb and M go out in MFMA A-operand order: block (m, n), lane
-        // l = 16 lq + lr, element e holds row 16 m + lr, column 16 n + 4 lq + e,
-        // so each lane of a scan wave reads its block with one float4 and the
-        // wave reads 1 KB contiguous.  Blocks above the diagonal are zero.
-        float* Tg = ws_T + cb * C * C;
-        float* Mg = ws_P + cb * C * C;
-        for (int q = tid; q < C * C / 4; q += 256) {
-            const int l = q & 63, blk = q >> 6;
-            const int bm = blk / NM, bn = blk % NM;
-            const int t = 16 * bm + (l & 15), i0 = 16 * bn + 4 * (l >> 4);
-            const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
-            f32x4 to, mo;
+            // Tb and M go out in MFMA A-operand order: block (m, n), lane
+            // l = 16 lq + lr, element e holds row 16 m + lr, column 16 n + 4 lq + e,
+            // so each lane of a scan wave reads its block with one float4 and the
+            // wave reads 1 KB contiguous.  Blocks above the diagonal are zero.
+            float* Tg = ws_T + cb * C * C;
+            float* Mg = ws_P + cb * C * C;
+            for (int q = tid; q < C * C / 4; q += 256) {
+                const int l = q & 63, blk = q >> 6;
+                const int bm = blk / NM, bn = blk % NM;
+                const int t = 16 * bm + (l & 15), i0 = 16 * bn + 4 * (l >> 4);
+                const f32x4 tv = ld4(Tm + t * LD + i0), bv = ld4(&b_w[w][i0]), mv = ld4(As + t * LD + i0);
+                f32x4 to, mo;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                to[e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
-                mo[e] = bn <= bm ? mv[e] : 0.f;
+                for (int e = 0; e < 4; ++e) {
+                    to[e] = i0 + e <= t ? tv[e] * bv[e] : 0.f;
+                    mo[e] = bn <= bm ? mv[e] : 0.f;
+                }
+                *reinterpret_cast<f32x4*>(Tg + 4 * q) = to;
+                *reinterpret_cast<f32x4*>(Mg + 4 * q) = mo;
             }
-            *reinterpret_cast<f32x4*>(Tg + 4 * q) = to;
-            *reinterpret_cast<f32x4*>(Mg + 4 * q) = mo;
         }
     }
 }
@@ -938,7 +962,8 @@ template <int SD, int C>
 static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks, float* wsT,
                            float* wsP, float* wsE, uint8_t* wsK, hipStream_t st) {
     constexpr bool SPLIT = C >= 32;
-    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C, SPLIT>), dim3(n_chunks, n_kh), dim3(256), 0, st,
+    const int n_items = n_chunks * n_kh;
+    hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C, SPLIT>), dim3(std::min(n_items, 2 * 256)), dim3(256), 0, st,
                        a, wsT, wsP, wsE, wsK, n_chunks);
     if constexpr (SPLIT)
         hipLaunchKernelGGL((delta_chunk_scan_bf_kernel<SD, C>), dim3(n_vh * (SD / 16)), dim3(256), 0, st,
