@@ -16,8 +16,16 @@ static int pick_gb(int G, int hd) {
     return 1;
 }
 
-// kv heads per workgroup: the largest power of two <= kWaves dividing Hkv.
+// kv heads per workgroup: the largest power of two <= kWaves dividing Hkv
+// (kWaves / hw waves share a head's tiles).  LMX_DECODE_HW = 1, 2 or 4
+// overrides it where it divides Hkv, for tuning sweeps.
 static int pick_hw(int Hkv) {
+    static const int env = [] {
+        const char* e = std::getenv("LMX_DECODE_HW");
+        const int v = e ? std::atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4) ? v : 0;
+    }();
+    if (env && Hkv % env == 0) return env;
     for (int hw = kWaves; hw > 1; hw >>= 1)
         if (Hkv % hw == 0) return hw;
     return 1;
