@@ -151,3 +151,20 @@ def test_delta_chunked_c5_full_size_matches_sequential_kernel():
     e_o = assert_close(o_chk, o_seq, what="o")
     e_s = assert_close(S_chk, S_seq, what="S")
     say(f"  o max_abs={e_o[0]:.2e} rel={e_o[1]:.2e}; S max_abs={e_s[0]:.2e} rel={e_s[1]:.2e}")
+
+
+@pytest.mark.parametrize("T", [2577, 6400])
+def test_delta_chunked_prep_items_per_workgroup(T):
+    """The chunk prep walks (chunk, k-head) items with a stride of its grid
+    (at most 512 workgroups) and prefetches each next item's rows: T=2577
+    gives 656 items (some workgroups take two, the rest one, and the last
+    chunk is ragged), T=6400 gives 1600 (three or four each).  Against the
+    token-sequential kernel, with a nonzero initial state."""
+    n_vh, n_kh, sd = 32, 16, 128
+    say(f"delta_chunked prep items T={T} items={-(-T // 64) * n_kh}")
+    conv, al, be, S0, A, dt = delta_inputs(T + 11, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.1)
+    o_seq, S_seq = _delta_gpu(lmx.delta_recur, conv, al, be, S0, A, dt, n_vh, n_kh, sd)
+    o_chk, S_chk = _delta_gpu(lmx.delta_chunked, conv, al, be, S0, A, dt, n_vh, n_kh, sd, chunk=64)
+    e_o = assert_close(o_chk, o_seq, what="o")
+    e_s = assert_close(S_chk, S_seq, what="S")
+    say(f"  o max_abs={e_o[0]:.2e} rel={e_o[1]:.2e}; S max_abs={e_s[0]:.2e} rel={e_s[1]:.2e}")
