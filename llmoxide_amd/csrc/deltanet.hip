@@ -257,9 +257,9 @@ struct ChunkSmem {
 // space.  Decays are handled in log2 units (exp2 is the native instruction).
 //
 // SPLIT (chunks of 32 and 64): Tb and M go out as split-bf16 pieces, and the
-// chunk's K and Q are written once more, split, in the scan's operand order
-// (K and Q rows for X and Y, K^T for the state update) to ws_K, so the 16
-// scan workgroups that read a k-head's chunk split nothing themselves.
+// chunk's K and Q rows are written once more, split, in the scan's operand
+// order for X and Y to ws_K, so the 16 scan workgroups that read a k-head's
+// chunk split nothing themselves (the scan forms K^T from its K tiles in LDS).
 template <int SD, int C, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
                                                                float* ws_P, float* ws_e,
@@ -364,28 +364,16 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
 
         if constexpr (SPLIT) {
             // K, Q pieces (token tile m, dim step sg): lane (lr, lq) row 16 m + lr,
-            // dims 32 sg + 4 lq + {0..3} and + 16.  K^T pieces (dim tile ct, token
-            // step sg): lane (lr, lq) dim 16 ct + lr, tokens 32 sg + 4 lq + {0..3}
-            // and + 16.  Staged rows past the chunk's end are zero.
-            constexpr int SX = SD / 32, SC = C / 32;
-            uint8_t* kb = ws_K + ((size_t)ch * a.n_kh + hk) * (3 * C * SD * 4);
+            // dims 32 sg + 4 lq + {0..3} and + 16.  Staged rows past the chunk's
+            // end are zero.
+            constexpr int SX = SD / 32;
+            uint8_t* kb = ws_K + ((size_t)ch * a.n_kh + hk) * (2 * C * SD * 4);
             for (int q = tid; q < NM * SX * 64; q += 256) {
                 const int l = q & 63, pc = q >> 6, m = pc / SX, sg = pc % SX;
                 const int t = 16 * m + (l & 15), c0 = 32 * sg + 4 * (l >> 4);
                 st_piece(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)));
                 st_piece(kb + C * SD * 4 + pc * kPiece, l,
                          split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)));
-            }
-            for (int q = tid; q < (SD / 16) * SC * 64; q += 256) {
-                const int l = q & 63, pc = q >> 6, ct = pc / SC, sg = pc % SC;
-                const int d = 16 * ct + (l & 15), t0 = 32 * sg + 4 * (l >> 4);
-                f32x4 x0, x1;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    x0[r] = Ks[(t0 + r) * KLD + d];
-                    x1[r] = Ks[(t0 + 16 + r) * KLD + d];
-                }
-                st_piece(kb + 2 * C * SD * 4 + pc * kPiece, l, split8(x0, x1));
             }
         }
 
@@ -745,13 +733,22 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(DeltaArgs a, cons
 
 // The scan on split-bf16 operands (chunks of 32 and 64 tokens): the same
 // work split and chunk algebra as delta_chunk_scan_kernel, every product a
-// 16x16x32 bf16 MFMA triple (mfma3).  K, Q, K^T, Tb and M arrive as pieces
+// 16x16x32 bf16 MFMA triple (mfma3).  K, Q, Tb and M arrive as pieces
 // from the prep kernel; the three operands formed here (Z, W = U exp(lg_C -
 // lg), and the updated state columns) are split once by the wave that
 // produces them and pass through LDS as bf16 hi/lo tiles in the D layout.
 // Each wave keeps its own state columns in fp32 (Sown) for the decay term
 // and the final store.  A piece register is reloaded with the next chunk's
 // piece right after its last use in this chunk.
+//
+// The K^T operand of the state update comes from LDS, not from pieces of its
+// own: each token wave writes the K tile it already holds for X (rows = its
+// 16 tokens) into Kth/Ktl [token][dim] (bf16 hi, lo), and after the Z
+// barrier every wave reads its K^T operand with ds_read_b64_tr_b16: in a
+// 16-lane group, lane a + 4 i addresses row t0 + i, dims 16 ct + 4 a .. + 3,
+// and lane L receives tokens t0 .. t0 + 3 of dim 16 ct + L.  That saves a
+// third of the K/Q piece bytes the prep writes and a quarter of the pieces
+// each scan workgroup reads from L2 per chunk.
 template <int SD, int C>
 __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, const uint8_t* ws_T,
                                                                   const uint8_t* ws_P,
@@ -759,11 +756,14 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
                                                                   const uint8_t* ws_K, int n_chunks) {
     constexpr int NT = SD / 16, NM = C / 16, TPW = NT / 4;
     constexpr int SX = SD / 32, SC = C / 32;  // 32-wide steps over dims, over tokens
-    constexpr size_t KQB = (size_t)3 * C * SD * 4;  // ws_K bytes per (chunk, k-head)
+    constexpr size_t KQB = (size_t)2 * C * SD * 4;  // ws_K bytes per (chunk, k-head)
     static_assert(NM % 2 == 0 && NT % 4 == 0, "whole 32-wide steps, whole column tiles per wave");
     __shared__ bf16x4 Zh[NM * 64], Zl[NM * 64];  // Z tiles, D layout
     __shared__ bf16x4 Wh[NM * 64], Wl[NM * 64];  // W tiles, D layout
     __shared__ bf16x4 Sh[NT * 64], Sl[NT * 64];  // state columns, D layout
+    constexpr int KTLD = SD + 4;                   // Kth/Ktl row stride (bf16), 8-byte rows
+    __shared__ __attribute__((aligned(16))) __bf16 Kth[C][KTLD];
+    __shared__ __attribute__((aligned(16))) __bf16 Ktl[C][KTLD];
     const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hv = blockIdx.x % a.n_vh, rb = blockIdx.x / a.n_vh;
@@ -801,8 +801,30 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
     Bf8 kx[SX], qx[SX], kt[TPW][SC], tb[SC], mm[SC];
     auto ld_kx = [&](int ch, int sg) { kx[sg] = ld_piece(kq_base(ch) + (m * SX + sg) * kPiece, lane); };
     auto ld_qx = [&](int ch, int sg) { qx[sg] = ld_piece(kq_base(ch) + C * SD * 4 + (m * SX + sg) * kPiece, lane); };
-    auto ld_kt = [&](int ch, int jj, int sg) {
-        kt[jj][sg] = ld_piece(kq_base(ch) + 2 * C * SD * 4 + ((TPW * w + jj) * SC + sg) * kPiece, lane);
+    // This wave's K tile (tokens 16 m + lr, dims 32 sg + 4 lq + {0..3}, + 16) to LDS
+    auto put_k = [&](int sg) {
+        const int t = 16 * m + lr, d0 = 32 * sg + 4 * lq;
+        *reinterpret_cast<bf16x4*>(&Kth[t][d0]) = __builtin_shufflevector(kx[sg].hi, kx[sg].hi, 0, 1, 2, 3);
+        *reinterpret_cast<bf16x4*>(&Kth[t][d0 + 16]) = __builtin_shufflevector(kx[sg].hi, kx[sg].hi, 4, 5, 6, 7);
+        *reinterpret_cast<bf16x4*>(&Ktl[t][d0]) = __builtin_shufflevector(kx[sg].lo, kx[sg].lo, 0, 1, 2, 3);
+        *reinterpret_cast<bf16x4*>(&Ktl[t][d0 + 16]) = __builtin_shufflevector(kx[sg].lo, kx[sg].lo, 4, 5, 6, 7);
+    };
+    // K^T operands of this wave's column tiles (dim 16 ct + lr, tokens 32 sg +
+    // 4 lq + {0..3}, + 16), transposed out of LDS
+    auto get_kt = [&]() {
+        typedef __attribute__((address_space(3))) bf16x4 lds_b4;
+        const int row = 4 * lq + (lr >> 2), col = 4 * (lr & 3);
+#pragma unroll
+        for (int jj = 0; jj < TPW; ++jj)
+#pragma unroll
+            for (int sg = 0; sg < SC; ++sg) {
+                const int r0 = 32 * sg + row, c0 = 16 * (TPW * w + jj) + col;
+                const bf16x4 h0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)&Kth[r0][c0]);
+                const bf16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)&Kth[r0 + 16][c0]);
+                const bf16x4 l0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)&Ktl[r0][c0]);
+                const bf16x4 l1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)&Ktl[r0 + 16][c0]);
+                kt[jj][sg] = join8(h0, h1, l0, l1);
+            }
     };
     auto ld_tb = [&](int ch, int sg) { tb[sg] = ld_piece(mat_base(ws_T, ch) + (m * SC + sg) * kPiece, lane); };
     auto ld_mm = [&](int ch, int sg) { mm[sg] = ld_piece(mat_base(ws_P, ch) + (m * SC + sg) * kPiece, lane); };
@@ -841,6 +863,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
             for (int sg = 0; sg < SX; ++sg) {
                 X = mfma3(kx[sg], sb[sg], X);
                 Y = mfma3(qx[sg], sb[sg], Y);
+                put_k(sg);
                 ld_kx(cn, sg);
                 ld_qx(cn, sg);
             }
@@ -853,7 +876,8 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
             Zh[m * 64 + lane] = h;
             Zl[m * 64 + lane] = l;
         }
-        __syncthreads();  // Z complete
+        __syncthreads();  // Z complete, and the chunk's K tile in LDS
+        get_kt();
 
         if (tok_wave) {
             // U = Tb Z and O = exp(lg) Y + M Z over the chunk's tokens
@@ -896,10 +920,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
             const Bf8 wb = join8(Wh[2 * sg * 64 + lane], Wh[(2 * sg + 1) * 64 + lane],
                                  Wl[2 * sg * 64 + lane], Wl[(2 * sg + 1) * 64 + lane]);
 #pragma unroll
-            for (int jj = 0; jj < TPW; ++jj) {
-                acc[jj] = mfma3(kt[jj][sg], wb, acc[jj]);
-                ld_kt(cn, jj, sg);
-            }
+            for (int jj = 0; jj < TPW; ++jj) acc[jj] = mfma3(kt[jj][sg], wb, acc[jj]);
         }
 #pragma unroll
         for (int jj = 0; jj < TPW; ++jj) Sown[jj] = acc[jj];
@@ -924,10 +945,6 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
             ld_mm(0, sg);
         }
     }
-#pragma unroll
-    for (int jj = 0; jj < TPW; ++jj)
-#pragma unroll
-        for (int sg = 0; sg < SC; ++sg) ld_kt(0, jj, sg);
     put_s();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
@@ -944,13 +961,13 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
 
 // Workspace: Tb and M [n_vh][n_chunks][chunk^2] floats (fp32 fragments, or
 // split-bf16 pieces of the same size), the decays [n_vh][n_chunks][2 chunk],
-// and, for the split path (chunks of 32 and 64), K, Q and K^T pieces
-// [n_chunks][n_kh][3 chunk s_dim] floats' worth.
+// and, for the split path (chunks of 32 and 64), K and Q pieces
+// [n_chunks][n_kh][2 chunk s_dim] floats' worth.
 static bool chunk_split(int chunk) { return chunk >= 32; }
 
 static size_t chunk_ws_floats(const lmx_dop* op, int chunk) {
     const size_t n_chunks = (op->n_tok + chunk - 1) / chunk;
-    const size_t kq = chunk_split(chunk) ? (size_t)op->n_kh * n_chunks * 3 * chunk * op->s_dim : 0;
+    const size_t kq = chunk_split(chunk) ? (size_t)op->n_kh * n_chunks * 2 * chunk * op->s_dim : 0;
     return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk) + kq;
 }
 

@@ -189,15 +189,15 @@ def test_deltanet_validation():
 @pytest.mark.parametrize("T,n_vh,n_kh,sd", [(4096, 32, 16, 128), (37, 4, 2, 64), (200, 8, 4, 128)])
 def test_deltanet_chunked_workspace_size(T, n_vh, n_kh, sd):
     # per (v-head, chunk): Tb and M (chunk^2 floats each) and the decays (2 chunk);
-    # chunks of 32 and 64 add the split-bf16 K, Q and K^T of every (chunk, k-head),
-    # 3 * chunk * s_dim floats' worth; all rounded up to 256 bytes
+    # chunks of 32 and 64 add the split-bf16 K and Q of every (chunk, k-head),
+    # 2 * chunk * s_dim floats' worth; all rounded up to 256 bytes
     L = lmx.lib()
     op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
     for chunk in (16, 32, 64):
         n_ch = (T + chunk - 1) // chunk
         floats = n_vh * n_ch * (2 * chunk * chunk + 2 * chunk)
         if chunk >= 32:
-            floats += n_kh * n_ch * 3 * chunk * sd
+            floats += n_kh * n_ch * 2 * chunk * sd
         want = (floats * 4 + 255) // 256 * 256
         assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk) == want
 
