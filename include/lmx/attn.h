@@ -60,7 +60,7 @@ typedef struct {
     uint32_t n_tokens;    /* t >= 1, queries at base_pos .. base_pos+t-1      */
     uint32_t n_heads;     /* H, a multiple of n_kv_heads                      */
     uint32_t n_kv_heads;  /* Hkv                                              */
-    uint32_t head_dim;    /* 64, 128, 256 or 512                              */
+    uint32_t head_dim;    /* a multiple of 4 up to 512 (see below)            */
     uint32_t kv_dim;      /* cache row stride in elements, >= Hkv*head_dim    */
     uint32_t base_pos;    /* position of the batch's first token              */
     uint32_t window;      /* 0 = global linear cache, else ring of `window`   */
@@ -97,6 +97,12 @@ const char *lmx_status_str(lmx_status s);
 
 /* Library version as 10000*major + 100*minor + patch. */
 int lmx_version(void);
+
+/* Kernel-choice overrides (LMX_PREFILL_KERNEL, LMX_PREFILL_GP, LMX_PREFILL_KH,
+ * LMX_DECODE_KROWS) are read from the environment once, at the first launch.
+ * This reads them again, for tests and tuning sweeps.  No reference
+ * counterpart.  Not to be called while another thread launches. */
+void lmx_tuning_reload(void);
 
 /* Zero a workspace (a fill kernel, not hipMemsetAsync, so the call may sit
  * inside a captured graph).  No entry point needs a zeroed workspace: each
@@ -177,6 +183,15 @@ lmx_status lmx_attn_prologue(const lmx_prologue_desc *d, float *q, const float *
  * lmx_workspace_init; 0 bytes may be asked for (ws may then be NULL).  It
  * holds the split partials of decode, and of prefill when a short batch on a
  * long cache is cut into key splits to fill the GPU.
+ * head_dim: the kernels run 64, 128, 256 and 512 natively (rows 16-byte
+ * aligned: kv_dim and q_stride multiples of 8, buffers 16-byte aligned).  Any
+ * other multiple of 4 up to 512 (the reference's vec4 domain, attn.wgsl:36-46;
+ * a vision tower's embedding_length / head_count) runs at the next native
+ * size on zero-padded copies of Q, of the cache rows the call reads and of
+ * k_cur/v_cur, held in the workspace, whose first head_dim output dims are
+ * copied to out (gated there): kv_dim and q_stride multiples of 4, the f16
+ * buffers 8-byte aligned.  The copies cost extra passes over those rows.
+ * lmx_attn_decode_batched takes native sizes only.
  */
 size_t lmx_attn_workspace_bytes(const lmx_attn_params *p);
 
@@ -197,9 +212,15 @@ lmx_status lmx_attn_fwd(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,
  * nothing, when the call needs more (lmx_attn_workspace_bytes(p) is the
  * need): a 32k-token decode at Qwen3-8B shape needs about 2 MiB, a
  * 512-token chunk on a 4k cache about 34 MiB.  No entry point allocates,
- * and this one takes no workspace either.  Every call on one GPU shares
- * that GPU's scratch, so calls that overlap on one GPU (concurrent streams,
- * or threads) race; serialize them on one stream. */
+ * and this one takes no workspace either.  The scratch used is that of the
+ * device `stream` belongs to (the current device for the null stream).
+ * Every call on one GPU shares that GPU's scratch, so calls that overlap on
+ * one GPU (concurrent streams, or threads) race; serialize them on one
+ * stream.  The array lives in the library's code object, so every process
+ * that loads the library holds it on each GPU the library runs on, whether
+ * or not it calls this entry point.  Its address is cached per device: after
+ * hipDeviceReset on a device, do not call this entry point there again in
+ * the same process. */
 #define LMX_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 lmx_status lmx_attn_fwd_noalloc(const lmx_attn_params *p, const void *q, lmx_dtype q_dt,

@@ -206,6 +206,7 @@ _PVP = ctypes.POINTER(ctypes.c_void_p)
 SIGNATURES = {
     "lmx_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "lmx_version": (ctypes.c_int, []),
+    "lmx_tuning_reload": (None, []),
     "lmx_workspace_init": (ctypes.c_int, [_VP, _SZ, _VP]),
     "lmx_kv_append": (ctypes.c_int, [_PK, _VP, _VP, _VP, _VP, ctypes.c_int, _VP]),
     "lmx_attn_prologue": (ctypes.c_int, [_PP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
@@ -260,6 +261,12 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def tuning_reload() -> None:
+    """Re-read the LMX_* kernel-choice overrides from the environment (the
+    library reads them once, at its first launch)."""
+    lib().lmx_tuning_reload()
 
 
 def _check(fn: str, rc: int) -> None:

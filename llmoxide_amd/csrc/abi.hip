@@ -4,7 +4,10 @@
 // anything and reports failures as lmx_status codes, mirroring the reference's
 // host-side checks (ensure! on batch and context, qwen35.rs:1212-1222;
 // forward.rs:1385-1395) and its error enum (llmoxide/src/error.rs:9-47).
+#include <atomic>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "common.hpp"
@@ -62,13 +65,25 @@ static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     return ca < cb + nb && cb < ca + na;
 }
 
+// attn_pad.hip: head sizes outside the kernels' set, through padded copies
+bool native_head_dim(uint32_t hd);
+size_t padded_workspace_bytes(const lmx_attn_params* p);
+lmx_status padded_attn(const lmx_attn_params* p, const AttnIo& io, const void* q, lmx_dtype q_dt,
+                       const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
+                       float* out, void* ws, size_t ws_bytes, hipStream_t st);
+
+// head_dim: a multiple of 4 up to 512, the reference's domain (vec4 rows,
+// attn.wgsl:36-46).  64, 128, 256 and 512 run natively; the others through
+// zero-padded copies at the next of those sizes.  Cache rows are a multiple
+// of 8 elements (16-byte loads) at native sizes, of 4 otherwise.
 static lmx_status check_attn_params(const lmx_attn_params* p) {
     if (!p) return LMX_E_NULL;
     if (p->n_tokens == 0 || p->n_heads == 0 || p->n_kv_heads == 0) return LMX_E_SHAPE;
     if (p->n_heads % p->n_kv_heads) return LMX_E_SHAPE;
-    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256 && p->head_dim != 512)
-        return LMX_E_UNSUPPORTED;
-    if ((uint64_t)p->kv_dim < (uint64_t)p->n_kv_heads * p->head_dim || p->kv_dim % 8) return LMX_E_SHAPE;
+    if (p->head_dim == 0 || p->head_dim > 512 || p->head_dim % 4) return LMX_E_UNSUPPORTED;
+    const uint32_t row_align = native_head_dim(p->head_dim) ? 8 : 4;
+    if ((uint64_t)p->kv_dim < (uint64_t)p->n_kv_heads * p->head_dim || p->kv_dim % row_align)
+        return LMX_E_SHAPE;
     if (!std::isfinite(p->scale)) return LMX_E_SHAPE;
     if (p->bidi > 1) return LMX_E_SHAPE;
     const uint64_t end = (uint64_t)p->base_pos + p->n_tokens;
@@ -81,7 +96,7 @@ static lmx_status check_attn_params(const lmx_attn_params* p) {
     return LMX_OK;
 }
 
-static bool use_split_k(const lmx_attn_params* p, lmx_dtype q_dt) {
+bool use_split_k(const lmx_attn_params* p, lmx_dtype q_dt) {
     return p->n_tokens <= kSplitKMaxTokens || !prefill_supported(p, q_dt);
 }
 
@@ -137,19 +152,51 @@ constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
 
-// The current device's copy of `scratch`, looked up once per device.
-static lmx_status scratch_of_current_device(void** out) {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LMX_E_DEVICE;
+// The copy of `scratch` on the device that `stream` belongs to (the null
+// stream: the current device), looked up once per device with that device
+// current.  The kernels run on the stream's device, so its copy is the one
+// they may touch.
+static lmx_status scratch_of_stream_device(hipStream_t stream, void** out) {
+    int cur = -1, dev = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur < 0) return LMX_E_DEVICE;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return LMX_E_DEVICE;
+    if (dev < 0 || dev >= kMaxDevices) return LMX_E_DEVICE;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
+        if (dev != cur && hipSetDevice(dev) != hipSuccess) return LMX_E_DEVICE;
         void* ptr = nullptr;
-        if (hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
-            return LMX_E_DEVICE;
+        const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !ptr) return LMX_E_DEVICE;
         g_scratch_ptr[dev] = ptr;
     }
     *out = g_scratch_ptr[dev];
     return LMX_OK;
+}
+
+// ---- tuning overrides (see Tuning in common.hpp)
+static std::atomic<int> g_tune_kernel{-1}, g_tune_gp{0}, g_tune_kh{-1}, g_tune_krows{-1};
+static std::once_flag g_tune_once;
+
+static void read_tuning_env() {
+    auto choice = [](const char* name, const char* a, int va, const char* b, int vb) {
+        const char* e = std::getenv(name);
+        if (e && !std::strcmp(e, a)) return va;
+        if (e && !std::strcmp(e, b)) return vb;
+        return -1;
+    };
+    g_tune_kernel.store(choice("LMX_PREFILL_KERNEL", "pp", 1, "tile", 0));
+    const char* gp = std::getenv("LMX_PREFILL_GP");
+    const int g = gp ? std::atoi(gp) : 0;
+    g_tune_gp.store((g == 1 || g == 2 || g == 4) ? g : 0);
+    const char* kh = std::getenv("LMX_PREFILL_KH");
+    g_tune_kh.store(kh && kh[0] == '0' ? 0 : -1);
+    g_tune_krows.store(choice("LMX_DECODE_KROWS", "1", 1, "0", 0));
+}
+
+Tuning tuning() {
+    std::call_once(g_tune_once, read_tuning_env);
+    return Tuning{g_tune_kernel.load(), g_tune_gp.load(), g_tune_kh.load(), g_tune_krows.load()};
 }
 
 }  // namespace lmx
@@ -176,7 +223,12 @@ const char* lmx_status_str(lmx_status s) {
     return "unknown status";
 }
 
-int lmx_version(void) { return 105; }
+int lmx_version(void) { return 106; }
+
+void lmx_tuning_reload(void) {
+    std::call_once(g_tune_once, [] {});
+    read_tuning_env();
+}
 
 lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     if (ws_bytes == 0) return LMX_OK;
@@ -265,6 +317,7 @@ lmx_status lmx_attn_prologue(const lmx_prologue_desc* d, float* q, const float* 
 
 size_t lmx_attn_workspace_bytes(const lmx_attn_params* p) {
     if (check_attn_params(p) != LMX_OK) return 0;
+    if (!native_head_dim(p->head_dim)) return padded_workspace_bytes(p);
     // The split-K decode path and a key-split prefill use a workspace; the
     // size covers whichever path either query dtype takes.
     size_t need = 0;
@@ -295,14 +348,17 @@ lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, con
     if ((k_cur == nullptr) != (v_cur == nullptr)) return LMX_E_NULL;
     if (p->window && p->n_tokens > 1 && (uint64_t)p->base_pos + p->n_tokens > p->window && !k_cur)
         return LMX_E_RING_HAZARD;
-    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 16))
+    // native sizes: 16-byte rows; padded ones are copied in 4-element pieces
+    const bool native = native_head_dim(p->head_dim);
+    const size_t qa = native || q_dt == LMX_F32 ? 16 : 8, ca = native ? 16 : 8;
+    if (!aligned(q, qa) || !aligned(k_cache, ca) || !aligned(v_cache, ca) || !aligned(out, 16))
         return LMX_E_ALIGN;
-    if (k_cur && (!aligned(k_cur, 16) || !aligned(v_cur, 16))) return LMX_E_ALIGN;
+    if (k_cur && (!aligned(k_cur, ca) || !aligned(v_cur, ca))) return LMX_E_ALIGN;
     const uint32_t hd = p->head_dim;
     const uint32_t qs = x && x->q_stride ? x->q_stride : hd;
     const uint32_t gs = x && x->gate_stride ? x->gate_stride : hd;
     const float* gate = x ? x->gate : nullptr;
-    if (qs < hd || qs % 8 || gs < hd || gs % 4) return LMX_E_SHAPE;
+    if (qs < hd || qs % (native ? 8 : 4) || gs < hd || gs % 4) return LMX_E_SHAPE;
     if ((uint64_t)p->n_tokens * p->n_heads * qs > INT32_MAX ||
         (uint64_t)p->n_tokens * p->n_heads * gs > INT32_MAX)
         return LMX_E_SHAPE;
@@ -316,6 +372,9 @@ lmx_status lmx_attn_fwd_ext(const lmx_attn_params* p, const lmx_attn_ext* x, con
     if (gate && overlaps(out, o_bytes, gate, (((size_t)p->n_tokens * p->n_heads - 1) * gs + hd) * 4))
         return LMX_E_SHAPE;
     const AttnIo io{(int)qs, (int)gs, gate};
+    if (!native)
+        return padded_attn(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
+                           (hipStream_t)stream);
     if (use_split_k(p, q_dt))
         return decode_fwd(p, io, q, q_dt, k_cache, v_cache, k_cur, v_cur, out, ws, ws_bytes,
                           (hipStream_t)stream);
@@ -333,7 +392,7 @@ lmx_status lmx_attn_fwd_noalloc(const lmx_attn_params* p, const void* q, lmx_dty
     if (need > kScratchBytes) return LMX_E_WORKSPACE;
     void* ws = nullptr;
     if (need > 0) {
-        s = scratch_of_current_device(&ws);
+        s = scratch_of_stream_device((hipStream_t)stream, &ws);
         if (s != LMX_OK) return s;
     }
     return lmx_attn_fwd_ext(p, nullptr, q, q_dt, k_cache, v_cache, kv_dt, k_cur, v_cur, out, ws,
@@ -358,6 +417,7 @@ lmx_status lmx_attn_decode_batched(const lmx_attn_params* p, int32_t n_seq, int3
     pp.base_pos = 0;
     lmx_status s = check_attn_params(&pp);
     if (s != LMX_OK) return s;
+    if (!native_head_dim(p->head_dim)) return LMX_E_UNSUPPORTED;  // no padded batched path
     if (p->bidi) return LMX_E_SHAPE;
     if (p->window == 0 && (uint32_t)max_ctx > p->n_slots) return LMX_E_CONTEXT;
     if (q_dt != LMX_F32 && q_dt != LMX_F16) return LMX_E_UNSUPPORTED;

@@ -74,10 +74,10 @@ static long min_tiles_per_wave(int hd) {
 // B=32 358 -> 336 us) or by a short stream (the 512-key C1 decode, 2 tiles a
 // wave: 8.05 -> 7.73 us).  One workgroup per CU streaming 16 tiles a wave
 // (B=1 at 32k) keeps the direct loads, 1% faster there (27.1 against 27.5 us
-// a call).  LMX_DECODE_KROWS=0|1 forces it (read on every call, for tests).
+// a call).  LMX_DECODE_KROWS=0|1 forces it (tuning overrides, for tests).
 static bool pick_krows(int hd, int mode, const DecodePlan& pl) {
     if (hd != 128 && hd != 256) return false;
-    if (const char* e = std::getenv("LMX_DECODE_KROWS")) return e[0] == '1';
+    if (const int f = tuning().decode_krows; f >= 0) return f == 1;
     const int tiles_per_wave = (pl.tps + kWaves / pl.hw - 1) / (kWaves / pl.hw);
     return mode == kModeBatched || pl.n_main > kCusPerGpu || tiles_per_wave <= 4;
 }

@@ -136,6 +136,20 @@ __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16
     }
 }
 
+// Q fragments as values defined here, not the registers of their loads (an
+// f16 query's conversions fold away): otherwise the waitcnt pass counts Q's
+// loads as possibly pending inside the key loop and puts vmcnt(n) waits
+// between the score MFMAs, which drain the K/V prefetch of later tiles.
+template <int N>
+__device__ __forceinline__ void settle_q(f16x8 (&qf)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(qf[i]));
+}
+
+// s_waitcnt vmcnt(0) as an instruction the compiler's waitcnt pass sees
+// (inline assembly it does not): every load issued before it is complete.
+__device__ __forceinline__ void drain_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
     const int q = n / 8, r = n % 8;
     const int xcd = bid % 8, local = bid / 8;
@@ -228,6 +242,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
             for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
         }
+        settle_q(qf);
     }
 
     // ---- key ranges: the workgroup's, and this wave's
@@ -603,6 +618,7 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kh_kernel(PrefillArgs a) 
 #pragma unroll
             for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
         }
+        settle_q(qf);
     }
 
     // ---- key ranges: the workgroup's, and this wave's
@@ -969,6 +985,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
 #pragma unroll
             for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
         }
+        settle_q(qf);
     }
 
     // ---- key tiles of the workgroup, and the wave's own run of them
@@ -1209,8 +1226,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
         }
     }
     // One loop per group (the group is fixed per wave); both run n_t + 1
-    // iterations of two barriers each.
+    // iterations of two barriers each.  The compiler joins the groups' paths
+    // (after the prologue, and from group 1's loop exit into group 0's
+    // preheader, never taken), so its waitcnt pass would see group 1's V
+    // fetch registers, which hold group 0's P, as pending in group 0's loop
+    // and wait for group 0's own K fetch before every P.V and exponential.
+    // Draining the loads before group 0's loop and after group 1's removes
+    // those waits.
     if (grp == 0) {
+        drain_loads();
         for (int i = 0; i <= n_t; ++i) {
             const int kt = kt_begin + i * BN;
             const bool k_in = i >= wi0 && i <= wi1;  // K tile i is the wave's (uniform)
@@ -1246,6 +1270,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
             if (v_in) pv(Vt_s + ((i + 1) & 1) * (HD * VPAD));
             __builtin_amdgcn_s_setprio(0);
         }
+        drain_loads();
     }
 
     // ---- normalize and store: o[nb][i] is dim nb*32 + 8*(i/4) + 4*hh + i%4
@@ -1270,26 +1295,20 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
 // per CU: it pays when there are at least two workgroups per CU (S >= 4096 at
 // 32 heads; at S = 2048 a single round of unequal causal workgroups leaves
 // CUs idle, and the 128-row kernel is faster).  LMX_PREFILL_KERNEL=pp|tile
-// forces one of them (read on every call, for tests and sweeps).
+// forces one of them (tuning overrides, for tests and sweeps).
 static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
     if (hd != 128) return false;
-    if (const char* e = std::getenv("LMX_PREFILL_KERNEL")) {
-        if (!std::strcmp(e, "pp")) return true;
-        if (!std::strcmp(e, "tile")) return false;
-    }
+    if (const int f = tuning().prefill_kernel; f >= 0) return f == 1;
     return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
 }
 
 // Query heads per prefill workgroup (they share one kv head).  At head_dim
 // >= 256 two heads of a kv group share a workgroup (64 rows each): a
 // 1024-key window then spans 34 key tiles per workgroup instead of 36, at
-// the same MFMA work per tile.  LMX_PREFILL_GP=1|2|4 overrides it (read on
-// every call, for tests and sweeps) where it divides G.
+// the same MFMA work per tile.  LMX_PREFILL_GP=1|2|4 overrides it (tuning
+// overrides, for tests and sweeps) where it divides G.
 static int prefill_gp(int hd, int G, bool pp) {
-    if (const char* e = std::getenv("LMX_PREFILL_GP")) {
-        const int v = std::atoi(e);
-        if ((v == 1 || v == 2 || v == 4) && G % v == 0) return v;
-    }
+    if (const int v = tuning().prefill_gp; v > 0 && G % v == 0) return v;
     if (pp) return 1;
     return hd >= 256 && G % 2 == 0 ? 2 : 1;
 }
@@ -1383,10 +1402,9 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     }
     // Key halves in one workgroup (attn_prefill_kh_kernel) when the 128-row
     // grid would fill at most half the CUs.  LMX_PREFILL_KH=0 turns it off
-    // (read on every call, for tests and A/B timing).
-    const char* kh_env = std::getenv("LMX_PREFILL_KH");
+    // (tuning overrides, for tests and A/B timing).
     const bool kh = !pp && hd <= 128 && lin && a.n_split == 1 && a.gp == 1 && 2 * nblk <= kPfCus &&
-                    !(kh_env && kh_env[0] == '0');
+                    tuning().prefill_kh != 0;
     if (kh) {
         a.n_qtiles = (a.n_tokens + 63) / 64;
         nblk = (long)a.n_qtiles * a.H;

@@ -77,6 +77,20 @@ __device__ __forceinline__ f32x4 gate_sigmoid4(f32x4 o, const float* g) {
                  gate_sigmoid(o[3], gv[3])};
 }
 
+// Kernel-choice overrides for tests and tuning sweeps, from the environment
+// (LMX_PREFILL_KERNEL = pp | tile, LMX_PREFILL_GP = 1 | 2 | 4,
+// LMX_PREFILL_KH = 0, LMX_DECODE_KROWS = 0 | 1).  Read once, at the first
+// launch, and again only by lmx_tuning_reload(): no getenv on the launch path,
+// so a launch and the workspace-size query it was sized by see the same
+// values.  -1 (or 0 for gp) means no override.
+struct Tuning {
+    int prefill_kernel;  // 1: ping-pong, 0: tile kernel
+    int prefill_gp;
+    int prefill_kh;      // 0: key halves off
+    int decode_krows;    // K rows through LDS (1) or direct operand loads (0)
+};
+Tuning tuning();  // the current overrides (abi.hip)
+
 // Load N consecutive f16 values (N a multiple of 4) as floats.
 template <int N>
 __device__ __forceinline__ void load_f16_as_f32(const f16* __restrict__ p, float (&out)[N]) {

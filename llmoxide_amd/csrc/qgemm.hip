@@ -18,8 +18,18 @@
 //   (|x - x_hi - x_lo| <= 2^-22 |x|), so each group's integer sum is two
 //   v_mfma_f32_32x32x16_f16 products accumulated in fp32, and the group's
 //   scale and offset are applied in fp32 (the x sums come from the fp32 x).
-//   |x| must stay below 65504, the f16 range (attention outputs over an f16
-//   V cache always do).
+//
+//   Range: before the split, each token's x is multiplied by a power of two
+//   2^k_t (exact).  k_t is the running minimum over the chunks of a bound
+//   k_c: 0 while the token's largest |x| in the chunk lies in [2^-6, 2^14),
+//   else the k that brings it into [2^14, 2^15).  So no scaled value comes
+//   near f16's 65504, and a token whose x are all tiny is scaled up instead
+//   of falling into f16 subnormals.  Every partial sum of a token is in one
+//   scaled domain: when a chunk changes k_t, the token's accumulated y is
+//   first multiplied by the (exact) ratio, and the store multiplies by
+//   2^-k_t.  Elements far below their chunk's maximum keep an absolute error
+//   of about 2^-22 of the largest value met, as fp32 summation would.  In
+//   the common case (k_t = 0 from the first chunk on) the scaling is skipped.
 //
 // Tiles.  A workgroup owns 64 tokens x 128 weight rows.  Its four consumer
 // waves multiply: wave (wm, wn) owns tokens 32 wm .. + 31 and rows
@@ -79,6 +89,24 @@ struct GemmArgs {
     int rows, in_dim, n_tok;
     size_t row_bytes;
 };
+
+// Largest x over each group of 32 lanes (x >= 0): DPP within each 16-lane
+// row, then one swizzle between the two rows of a group (no LDS traffic,
+// unlike ds_bpermute).
+__device__ __forceinline__ float max32(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp<0x141>(x));  // row_half_mirror
+    x = fmaxf(x, dpp<0x140>(x));  // row_mirror
+    // swizzle, bitmask mode: lane ^ 16 within 32
+    return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F)));
+}
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+__device__ __forceinline__ float sum8(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    return x + dpp<0x141>(x);  // row_half_mirror: lane i with 7 - i of its 8
+}
 
 // Swizzled offset (in halfs) of 8-half chunk c of LDS row r: the chunk index
 // is XORed with the row, so the rows an MFMA operand read touches spread
@@ -267,6 +295,10 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) f16 q_s[2][kGN * kGK];
     __shared__ __attribute__((aligned(16))) f32x2 so_s[2][kGN * NG];        // (s, o) per row, group
     __shared__ __attribute__((aligned(16))) float xs_s[2][OFFSET ? NG * kGM : 4];  // x sums per group, token
+    // Per token: the ratio 2^(k_new - k_old) of its x scale in this chunk,
+    // and 2^-k_new.
+    __shared__ __attribute__((aligned(16))) float rs_s[2][kGM];
+    __shared__ __attribute__((aligned(16))) float iv_s[2][kGM];
 
     const int n_tb = (a.n_tok + kGM - 1) / kGM;
     const int tb = blockIdx.x % n_tb, rb = blockIdx.x / n_tb;
@@ -290,6 +322,12 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
         // consecutive threads read one token's 512 contiguous bytes.
         constexpr int XT = g_xthreads<TY>(), XU = kGXF / XT;  // x-producer threads, float4s a thread
         f32x4 rx[XU];
+        // Running scale exponent k_t of each of this thread's tokens (100:
+        // no nonzero x seen yet; any ratio applied to a zero y is exact).
+        int kx[XU];
+#pragma unroll
+        for (int u = 0; u < XU; ++u) kx[u] = 100;
+        bool ones[2] = {false, false};  // buffer b holds (1, 1) for this wave's tokens (wave-uniform)
         constexpr bool Q8PAIR = TY == kGQ8_0 && WU == 2;
         uint32_t rw[WU][Q8PAIR ? 18 : WW];
         const int w_row = ptid / WPARTS, w_part = ptid % WPARTS;
@@ -328,26 +366,69 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
                 }
                 return;
             }
-#pragma unroll
-            for (int u = 0; u < XU; ++u) {
+            // x (scaled by 2^kn) to f16 hi / lo rows, the token's ratio and
+            // inverse scale, and (Q4_K) the group sums
+            auto emit = [&](int u, const f32x4& xv, float ratio, int kn, bool store_scale) {
                 const int i = ptid + XT * u, tok = i >> 5, k4 = i & 31;
+                if (store_scale && k4 == 0) {
+                    rs_s[b][tok] = ratio;
+                    iv_s[b][tok] = __builtin_amdgcn_ldexpf(1.f, -kn);
+                }
                 f16x4 hi, lo;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    hi[j] = (f16)rx[u][j];
-                    lo[j] = (f16)(rx[u][j] - (float)hi[j]);
+                    hi[j] = (f16)xv[j];
+                    lo[j] = (f16)(xv[j] - (float)hi[j]);
                 }
                 const int off = sw(tok, k4 >> 1) + 4 * (k4 & 1);
                 *reinterpret_cast<f16x4*>(&xh_s[b][off]) = hi;
                 *reinterpret_cast<f16x4*>(&xl_s[b][off]) = lo;
                 if constexpr (OFFSET) {
-                    // the group's x sum: eight consecutive lanes hold its 32 floats
-                    float sx = (rx[u][0] + rx[u][1]) + (rx[u][2] + rx[u][3]);
-                    sx += shfl_xor(sx, 1);
-                    sx += shfl_xor(sx, 2);
-                    sx += shfl_xor(sx, 4);
+                    // the group's (scaled) x sum: eight consecutive lanes hold its 32 floats
+                    float sx = (xv[0] + xv[1]) + (xv[2] + xv[3]);
+                    sx = sum8(sx);
                     if ((k4 & 7) == 0) xs_s[b][(k4 >> 3) * kGM + tok] = sx;
                 }
+            };
+            // Scale rule per (token, chunk), m the token's largest |x| in the
+            // chunk: k_c = 0 for m in [2^-6, 2^14), else 15 - e(m) with
+            // m < 2^e (so m 2^k_c lies in [2^14, 2^15)); no bound for m = 0
+            // or m not finite; k_t = min(k_t, k_c) from k_t = 100.  Once
+            // k_t = 0 and no |x| of the chunk reaches 2^14, k_t stays 0, so a
+            // wave whose tokens are all there skips the reduction and the
+            // scaling (the common case after the first chunk).
+            float ml[XU];
+            bool slow = false;
+#pragma unroll
+            for (int u = 0; u < XU; ++u) {
+                ml[u] = fmaxf(fmaxf(fabsf(rx[u][0]), fabsf(rx[u][1])), fmaxf(fabsf(rx[u][2]), fabsf(rx[u][3])));
+                slow |= !(ml[u] < 16384.f) || kx[u] != 0;
+            }
+            if (__builtin_amdgcn_ballot_w64(slow) == 0) {
+                // the wave's tokens keep scale 1: their (ratio, 1 / scale)
+                // entries need writing only if buffer b does not hold (1, 1)
+                const bool store = !ones[b];
+#pragma unroll
+                for (int u = 0; u < XU; ++u) emit(u, rx[u], 1.f, 0, store);
+                ones[b] = true;
+                return;
+            }
+            ones[b] = false;
+#pragma unroll
+            for (int u = 0; u < XU; ++u) {
+                // the token's 128 floats are on 32 consecutive lanes
+                const float m = max32(ml[u]);
+                int kn = kx[u];
+                if (m > 0.f && m <= 3.402823466e38f && !(m >= 0.015625f && m < 16384.f))
+                    kn = min(kn, 15 - __builtin_amdgcn_frexp_expf(m));
+                else if (m >= 0.015625f && m < 16384.f)
+                    kn = min(kn, 0);
+                const float ratio = __builtin_amdgcn_ldexpf(1.f, kn - kx[u]);
+                kx[u] = kn;
+                f32x4 xv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xv[j] = __builtin_amdgcn_ldexpf(rx[u][j], kn);
+                emit(u, xv, ratio, kn, true);
             }
         };
         load_chunk(0);
@@ -376,8 +457,24 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
         for (int j = 0; j < 16; ++j) y[n][j] = 0.f;
 
     __syncthreads();  // chunk 0 is stashed
+    // tokens of register j: 8 (j / 4) + 4 hh + j % 4 of the wave's 32
+    auto token_vals = [&](const float* src, f32x4 (&v)[4]) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[q4] = *reinterpret_cast<const f32x4*>(src + 32 * wm + 8 * q4 + 4 * hh);
+    };
     for (int ch = 0; ch < n_chunks; ++ch) {
         const int b = ch & 1;
+        // y so far moves to each token's scale of this chunk (a power of two,
+        // exact; 1 unless the chunk lowered it).  Unconditional: a branch on
+        // a change flag costs the Q6_K consumer spills.
+        {
+            f32x4 rt[4];
+            token_vals(rs_s[b], rt);
+#pragma unroll
+            for (int n = 0; n < kNTW; ++n)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) y[n][j] *= rt[j >> 2][j & 3];
+        }
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             f32x16 acc[kNTW];
@@ -419,6 +516,10 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
         __syncthreads();  // chunk ch's operands are read; chunk ch + 1 is stashed
     }
 
+    // back from each token's final x scale (the last chunk's buffer is not
+    // written again)
+    f32x4 iv[4];
+    token_vals(iv_s[(n_chunks - 1) & 1], iv);
 #pragma unroll
     for (int n = 0; n < kNTW; ++n) {
         const int r = r0 + 32 * kNTW * wn + 32 * n + l32;
@@ -426,7 +527,7 @@ __global__ __launch_bounds__(g_threads<TY>(), 1) void qgemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int t = t0 + 32 * wm + 8 * (j >> 2) + 4 * hh + (j & 3);
-            if (t < a.n_tok) a.y[(size_t)t * a.rows + r] = y[n][j];
+            if (t < a.n_tok) a.y[(size_t)t * a.rows + r] = y[n][j] * iv[j >> 2][j & 3];
         }
     }
 }

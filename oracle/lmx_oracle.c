@@ -306,8 +306,14 @@ int orc_attention(const orc_attn *p, const float *q, const float *k,
         orc_attn_run(&jobs[0]);
         return 0;
     }
-    for (int t = 0; t < n_threads; ++t) pthread_create(&th[t], NULL, orc_attn_run, &jobs[t]);
-    for (int t = 0; t < n_threads; ++t) pthread_join(th[t], NULL);
+    /* a thread that fails to start has its slice run here instead */
+    int started[256];
+    for (int t = 0; t < n_threads; ++t) {
+        started[t] = pthread_create(&th[t], NULL, orc_attn_run, &jobs[t]) == 0;
+        if (!started[t]) orc_attn_run(&jobs[t]);
+    }
+    for (int t = 0; t < n_threads; ++t)
+        if (started[t]) pthread_join(th[t], NULL);
     return 0;
 }
 
@@ -402,9 +408,15 @@ void orc_delta_recur_mt(const orc_dop *op, const float *ssm_a, const float *dt_b
         orc_delta_job j = {op, ssm_a, dt_bias, alpha, beta, conv, S, out,
                            (int64_t)op->n_vh * t / n_threads, (int64_t)op->n_vh * (t + 1) / n_threads};
         jobs[t] = j;
-        pthread_create(&th[t], NULL, orc_delta_run, &jobs[t]);
     }
-    for (int t = 0; t < n_threads; ++t) pthread_join(th[t], NULL);
+    /* a thread that fails to start has its slice run here instead */
+    int started[256];
+    for (int t = 0; t < n_threads; ++t) {
+        started[t] = pthread_create(&th[t], NULL, orc_delta_run, &jobs[t]) == 0;
+        if (!started[t]) orc_delta_run(&jobs[t]);
+    }
+    for (int t = 0; t < n_threads; ++t)
+        if (started[t]) pthread_join(th[t], NULL);
 }
 
 /* ops.rs:197-203: x / max(||x||, eps), per head of `dim` elements. */

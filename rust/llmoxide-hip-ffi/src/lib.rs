@@ -170,6 +170,8 @@ pub struct LmxKvm {
 extern "C" {
     pub fn lmx_status_str(s: i32) -> *const c_char;
     pub fn lmx_version() -> i32;
+    /// Re-reads the LMX_* kernel-choice overrides (tests and tuning sweeps).
+    pub fn lmx_tuning_reload();
     pub fn lmx_workspace_init(ws: *mut c_void, ws_bytes: usize, stream: HipStream) -> i32;
 
     /// The two `write_cache` dispatches (ops.wgsl:323-346; qwen35.rs:1062-1074,

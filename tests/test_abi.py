@@ -32,7 +32,7 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
 def test_library_exports_every_declared_symbol():
     L = lmx.lib()
     names = declared_functions()
-    assert len(names) == 30
+    assert len(names) == 31
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(lmx.SIGNATURES)
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = lmx.lib()
-    assert L.lmx_version() == 105
+    assert L.lmx_version() == 106
     for s in lmx.Status:
         assert L.lmx_status_str(int(s))
     assert L.lmx_status_str(999) == b"unknown status"
@@ -66,8 +66,12 @@ def _fwd(p, q=FAKE, k=FAKE, v=FAKE, out=FAKE + (1 << 24), kc=None, vc=None, qdt=
 @pytest.mark.parametrize("kw,code", [
     (dict(n_tokens=0), lmx.Status.E_SHAPE),
     (dict(n_heads=30), lmx.Status.E_SHAPE),
-    (dict(head_dim=96), lmx.Status.E_UNSUPPORTED),
+    (dict(head_dim=514), lmx.Status.E_UNSUPPORTED),
+    (dict(head_dim=98), lmx.Status.E_UNSUPPORTED),
+    (dict(head_dim=0, scale=1.0), lmx.Status.E_UNSUPPORTED),
     (dict(kv_dim=512), lmx.Status.E_SHAPE),
+    (dict(kv_dim=8 * 128 + 4), lmx.Status.E_SHAPE),        # native rows: multiples of 8
+    (dict(head_dim=72, kv_dim=8 * 72 + 2), lmx.Status.E_SHAPE),  # padded rows: of 4
     (dict(base_pos=16), lmx.Status.E_CONTEXT),
     (dict(n_tokens=17), lmx.Status.E_CONTEXT),
     (dict(window=32, n_slots=16), lmx.Status.E_SHAPE),
@@ -342,7 +346,7 @@ def test_noalloc_validates_and_refuses_shapes_beyond_its_scratch():
         return L.lmx_attn_fwd_noalloc(ctypes.byref(p), q, lmx.F32, FAKE, FAKE, lmx.F16, None, None,
                                       out, None)
     assert call(_params(n_tokens=0)) == lmx.Status.E_SHAPE
-    assert call(_params(head_dim=96)) == lmx.Status.E_UNSUPPORTED
+    assert call(_params(head_dim=514)) == lmx.Status.E_UNSUPPORTED
     limit = 64 << 20
     # the configured shapes fit: C2 decode at 32k, a C3 512-token chunk on 4k
     for kw in (dict(n_slots=32768, base_pos=32767), dict(n_tokens=512, n_slots=4608, base_pos=4096)):
@@ -355,3 +359,28 @@ def test_noalloc_validates_and_refuses_shapes_beyond_its_scratch():
     big = [p for p in candidates if L.lmx_attn_workspace_bytes(ctypes.byref(p)) > limit]
     assert big
     assert call(big[0]) == lmx.Status.E_WORKSPACE
+
+
+def test_padded_head_dims_validate_and_size_their_copies():
+    """head_dim outside 64/128/256/512 (a multiple of 4 up to 512) is taken
+    through zero-padded copies held in the workspace: the size query covers
+    them, a call without that workspace is refused before any device work,
+    the rows may be 4-element (8-byte) aligned, and the batched decode keeps
+    native sizes only."""
+    L = lmx.lib()
+    for hd in (4, 72, 80, 96, 200, 500):
+        p = _params(head_dim=hd, kv_dim=8 * hd, n_tokens=40, n_slots=300, base_pos=260)
+        need = L.lmx_attn_workspace_bytes(ctypes.byref(p))
+        hp = 64 if hd <= 64 else 128 if hd <= 128 else 256 if hd <= 256 else 512
+        # at least the padded Q, K, V and out
+        assert need >= 40 * 32 * hp * 4 + 2 * 300 * 8 * hp * 2 + 40 * 32 * hp * 4, (hd, need)
+        assert _fwd(p) == lmx.Status.E_WORKSPACE
+    # 4-element rows and 8-byte aligned f16 buffers pass validation
+    p = _params(head_dim=72, n_heads=1, n_kv_heads=1, kv_dim=76, n_tokens=3, n_slots=10, base_pos=7)
+    assert _fwd(p, k=FAKE + 8, v=FAKE + 8) == lmx.Status.E_WORKSPACE
+    assert _fwd(p, k=FAKE + 4) == lmx.Status.E_ALIGN
+    # native sizes keep 16-byte rows
+    assert _fwd(_params(), k=FAKE + 8) == lmx.Status.E_ALIGN
+    pb = _params(head_dim=72)
+    assert L.lmx_attn_decode_batched(ctypes.byref(pb), 1, 16, FAKE, FAKE, FAKE, FAKE, lmx.F32,
+                                     lmx.F16, FAKE + (1 << 24), None, 0, None) == lmx.Status.E_UNSUPPORTED

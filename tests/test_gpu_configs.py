@@ -57,10 +57,10 @@ def dev(a, dtype=None):
 
 
 @pytest.fixture(params=["tile", "pp"])
-def prefill_kernel(request, monkeypatch):
+def prefill_kernel(request, tuning_env):
     """Prefill cases run on both prefill kernels (the ping-pong kernel exists
     for head_dim 128; other head sizes take the tile kernel either way)."""
-    monkeypatch.setenv("LMX_PREFILL_KERNEL", request.param)
+    tuning_env("LMX_PREFILL_KERNEL", request.param)
     return request.param
 
 

@@ -192,7 +192,7 @@ def test_one_workspace_serves_every_entry_point():
     (32, 8, 128, 32768, 0, 1, False), (32, 8, 128, 700, 0, 1, True), (32, 8, 128, 1500, 1024, 1, False),
     (32, 8, 128, 3000, 0, 4, False),
     (16, 8, 256, 1500, 1024, 1, True), (16, 8, 256, 5000, 0, 1, False), (16, 8, 256, 900, 0, 3, True)])
-def test_k_operand_paths(H, Hkv, hd, ctx, window, t, q_f16, monkeypatch):
+def test_k_operand_paths(H, Hkv, hd, ctx, window, t, q_f16, tuning_env):
     """K tiles both ways (head_dim 128 and 256), forced: loaded row-major and
     turned into MFMA operands through LDS, or each lane's operand bytes loaded
     directly.  The operands are the same, so the outputs are the same bits."""
@@ -204,7 +204,7 @@ def test_k_operand_paths(H, Hkv, hd, ctx, window, t, q_f16, monkeypatch):
     ref = c.reference(base_pos=base, window=window)
     outs = []
     for krows in ("0", "1"):
-        monkeypatch.setenv("LMX_DECODE_KROWS", krows)
+        tuning_env("LMX_DECODE_KROWS", krows)
         say(f"K operand path krows={krows} ctx={ctx} w={window} t={t}")
         out = lmx.attention(q, kd, vd, n_heads=H, n_kv_heads=Hkv, head_dim=hd, base_pos=base, window=window)
         torch.cuda.synchronize()

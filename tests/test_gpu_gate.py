@@ -94,9 +94,9 @@ def test_strided_queries_without_gate(t):
 
 
 @pytest.mark.parametrize("q_f16", [False, True])
-def test_prefill_ping_pong_kernel_gated(q_f16, monkeypatch):
+def test_prefill_ping_pong_kernel_gated(q_f16, tuning_env):
     # the head_dim-128 ping-pong prefill kernel, forced at a small size
-    monkeypatch.setenv("LMX_PREFILL_KERNEL", "pp")
+    tuning_env("LMX_PREFILL_KERNEL", "pp")
     run(8, t=300, H=8, Hkv=2, hd=128, n_pos=340, base=40, q_f16=q_f16)
 
 

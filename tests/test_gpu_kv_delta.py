@@ -82,8 +82,11 @@ def test_delta_recur(n_vh, n_kh, sd, T, s0):
     assert_close(S, S_ref, what="S")
 
 
-@pytest.mark.parametrize("T,chunk", [(37, 16), (64, 64), (200, 64), (256, 32)])
+@pytest.mark.parametrize("T,chunk", [(37, 16), (64, 64), (200, 64), (256, 32), (250, 32), (99, 32)])
 def test_delta_chunked_matches_sequential(T, chunk):
+    # (250, 32) and (99, 32): a ragged last chunk at C = 32, where the scan's
+    # K^T operand comes from LDS rows the token waves wrote and the rows past
+    # T only from zero-filled prep pieces
     n_vh, n_kh, sd = 8, 4, 128
     say(f"delta_chunked T={T} chunk={chunk}")
     conv, al, be, S0, A, dt = delta_inputs(T + 7, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.2)

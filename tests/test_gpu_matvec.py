@@ -127,3 +127,39 @@ def test_matvec_and_gemm_agree_across_the_threshold(name):
     # 15 tokens take the matvec tiles, 16 the GEMM: both match the oracle
     for n_tok in (15, 16):
         run(name, 256, 1024, n_tok, seed=60)
+
+
+@pytest.mark.parametrize("name", GEMM_TYPES)
+def test_gemm_x_range(name):
+    # x outside f16's comfortable range, per token: large (|x| ~ 1e5, past
+    # f16's 65504), tiny (~1e-6, f16 subnormals), and rows whose 128-weight
+    # chunks grow or shrink by 11 orders of magnitude along the row (the
+    # running per-token scale).  Each token is checked against its own
+    # largest |ref|, so tiny tokens need full relative precision.
+    rows, in_dim, n_tok = 130, 1024, 64
+    say(f"gemm {name} x range rows={rows} in_dim={in_dim} n_tok={n_tok}")
+    ty = oracle.QTYPES[name]
+    w = oracle.quant_weights(ty, rows, in_dim, 80)
+    x = oracle.normal(81, (n_tok, in_dim)).astype(np.float64)
+    ramp = np.logspace(-6, 5, in_dim // 128).repeat(128)
+    for t in range(n_tok):
+        kind = t % 5
+        if kind == 1:
+            x[t] *= 1e5
+        elif kind == 2:
+            x[t] *= 1e-6
+        elif kind == 3:
+            x[t] *= ramp
+        elif kind == 4:
+            x[t] *= ramp[::-1]
+    x = x.astype(np.float32)
+    ref = oracle.matvec(ty, w, rows, in_dim, x)
+    y = lmx.matvec(torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(), qtype=name, rows=rows,
+                   in_dim=in_dim)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    for t in range(n_tok):
+        err = np.abs(got[t] - ref[t]).max()
+        scale = np.abs(ref[t]).max()
+        assert err <= 3e-5 * scale, f"{name} token {t} (kind {t % 5}): max err {err} vs max |ref| {scale}"

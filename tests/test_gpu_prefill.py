@@ -20,11 +20,11 @@ import llmoxide_amd as lmx  # noqa: E402
 
 
 @pytest.fixture(autouse=True, params=["tile", "pp"])
-def prefill_kernel(request, monkeypatch):
+def prefill_kernel(request, tuning_env):
     """Every case on both prefill kernels: the 128-row tile kernel and the
     ping-pong kernel (head_dim 128 only; other head sizes use the tile kernel
     under either setting)."""
-    monkeypatch.setenv("LMX_PREFILL_KERNEL", request.param)
+    tuning_env("LMX_PREFILL_KERNEL", request.param)
     return request.param
 
 
@@ -105,11 +105,11 @@ def test_prefill_head_geometries(H, Hkv, hd):
 @pytest.mark.parametrize("gp,H,Hkv,hd,window", [
     (gp, H, Hkv, hd, w) for (H, Hkv, hd, w) in [(16, 4, 128, 0), (16, 4, 128, 150), (8, 2, 256, 0), (16, 8, 256, 300)]
     for gp in (1, 2, 4) if (H // Hkv) % gp == 0])
-def test_prefill_heads_per_workgroup(gp, H, Hkv, hd, window, monkeypatch):
+def test_prefill_heads_per_workgroup(gp, H, Hkv, hd, window, tuning_env):
     """Query heads of one kv group packed into a workgroup (128 / gp rows
     each): ragged t, a window, and a ring with k_cur rows, against the oracle.
     gp takes every value in {1, 2, 4} that divides the group size."""
-    monkeypatch.setenv("LMX_PREFILL_GP", str(gp))
+    tuning_env("LMX_PREFILL_GP", str(gp))
     c = AttnCase(gp * 1000 + H + hd + window, t=333, H=H, Hkv=Hkv, hd=hd, n_pos=333 + 400, q_f16=True)
     say(f"heads per workgroup gp={gp}")
     if window:
@@ -189,11 +189,11 @@ def test_head_dim_512_sliding_window_with_k_cur():
     (8, 4, 64, 250, 0, 0, True, False, True),       # bidirectional
     (16, 4, 128, 9, 0, 0, False, False, True),      # fewer rows than a tile
 ])
-def test_key_halves_prefill(kh, H, Hkv, hd, t, base, window, bidi, kcur, qf16, monkeypatch):
+def test_key_halves_prefill(kh, H, Hkv, hd, t, base, window, bidi, kcur, qf16, tuning_env):
     """Short batches: each workgroup's two wave pairs walk the two halves of
     its key tiles and merge through LDS (kh=1), against the oracle; kh=0 is
     the one-chain kernel on the same inputs."""
-    monkeypatch.setenv("LMX_PREFILL_KH", kh)
+    tuning_env("LMX_PREFILL_KH", kh)
     c = AttnCase(t + base + hd + window, t=t, H=H, Hkv=Hkv, hd=hd, n_pos=base + t, q_f16=qf16,
                  qk_norm=True)
     check(c, base=base, window=window, bidi=bidi, ring=kcur, k_cur=kcur)
