@@ -29,7 +29,8 @@ CPU baseline: the C restatement of the reference's scalar loops (oracle/,
 cpu.rs:342-387 for attention, qwen35/cpu.rs:188-246 for the delta rule),
 compiled -O2 without fast-math, timed on this host on a bounded sample of
 each config, on one core (the reference's attention loop is serial) and on
-all the cores this process may use (threads over heads), up to 16.
+all the cores this process may use (threads over heads), up to 16 (one GPU's
+share of the host); the host's own CPU count and model are printed beside.
 """
 from __future__ import annotations
 
@@ -244,8 +245,11 @@ def bench_prefill(lmx, torch, S, base=0, Hq=H, Hkv=HKV, hd=HD, window=0, scale=N
     return e
 
 
-def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5):
-    Hq, Hkv, hd = 16, 8, 256
+def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5, Hkv=8, hd=256, scale=1 / 16):
+    """Gemma-shape decode at 32k context.  Defaults: C4 (H 16, Hkv 8, hd 256,
+    scale 1/16); Gemma 4's real global layers are Hkv 1, hd 512, scale 1.0
+    (ARCHITECTURE.md:25-28).  8 rotated layer caches."""
+    Hq = 16
     slots = window or CTX
     n_layers = 8
     ks = [torch.randn((slots, Hkv * hd), dtype=torch.float16, device="cuda") for _ in range(n_layers)]
@@ -254,10 +258,11 @@ def bench_gemma_decode(lmx, torch, window, steps=50, warmup=5):
     out = torch.empty((1, Hq * hd), dtype=torch.float32, device="cuda")
     ws = lmx.Workspace()
     fns = [(lambda i=i: lmx.attention(q, ks[i], vs[i], n_heads=Hq, n_kv_heads=Hkv, head_dim=hd,
-                                      base_pos=CTX - 1, window=window, scale=1 / 16, out=out, workspace=ws))
+                                      base_pos=CTX - 1, window=window, scale=scale, out=out, workspace=ws))
            for i in range(n_layers)]
     ms, med = time_calls(fns, steps, warmup, torch)
-    return hbm_entry(decode_bytes([min(window or CTX, CTX)], Hq, Hkv, hd), ms, med, window=window)
+    return hbm_entry(decode_bytes([min(window or CTX, CTX)], Hq, Hkv, hd), ms, med, window=window,
+                     n_kv_heads=Hkv, head_dim=hd, scale=scale)
 
 
 def bench_prologue(lmx, torch, t, H=H, Hkv=HKV, hd=HD, steps=20, warmup=3):
@@ -379,6 +384,26 @@ def cpu_cores_all():
     return max(1, min(16, n))
 
 
+def host_cpu_info():
+    """The host's logical CPU count, the count this process may run on, and
+    the CPU model (from /proc/cpuinfo), reported beside the CPU baselines."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"logical_cpus": os.cpu_count(), "cpus_allowed": affinity, "model": model,
+            "threads_used_all_cores": cpu_cores_all()}
+
+
 _KV_CACHE = {}
 
 
@@ -491,6 +516,13 @@ def cpu_baselines(budget_s):
     both("gemma_decode_global", lambda th: cpu_attention_rows(
         [CTX - 1] * 50, Hq=16, Hkv=8, hd=256, n_pos=CTX, scale=1 / 16, unit="GB/s", threads=th,
         budget_s=budget_s, what="C4 global decode at 32k"))
+    _cpu_kv(CTX, 512, 11)
+    both("gemma4_global_prefill_4k_hd512", lambda th: cpu_attention_rows(
+        spread(4096, 0, 64), Hq=16, Hkv=1, hd=512, n_pos=4096, scale=1.0, unit="TFLOP/s", threads=th,
+        budget_s=budget_s, what="Gemma 4 global layer prefill 4k (hd 512, one kv head)"))
+    both("gemma4_global_decode_32k_hd512", lambda th: cpu_attention_rows(
+        [CTX - 1] * 50, Hq=16, Hkv=1, hd=512, n_pos=CTX, scale=1.0, unit="GB/s", threads=th,
+        budget_s=budget_s, what="Gemma 4 global layer decode at 32k (hd 512, one kv head)"))
 
     def delta(th, T, name):
         per_tok = cpu_delta(64, th, budget_s)
@@ -557,6 +589,15 @@ def main():
             ("gemma_prefill_global_4k", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=8, hd=256,
                                                               scale=1 / 16, qk_norm=False, steps=5,
                                                               warmup=1)),
+            # Gemma 4's real global layers: hd 512, one kv head, scale 1.0 on
+            # RMS-normed q and k (ARCHITECTURE.md:25-28, 54-62); FLOPs are the
+            # algorithmic 4*hd*H per visible pair, not the 1.5x the two
+            # output-dim workgroups of a (head, tile) issue
+            ("gemma4_global_prefill_4k_hd512", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=1, hd=512,
+                                                                     scale=1.0, qk_norm=True, steps=5,
+                                                                     warmup=1)),
+            ("gemma4_global_decode_32k_hd512", lambda: bench_gemma_decode(lmx, torch, 0, Hkv=1, hd=512,
+                                                                          scale=1.0)),
             ("prologue_prefill_t4096", lambda: bench_prologue(lmx, torch, 4096)),
             ("prologue_decode_t1", lambda: bench_prologue(lmx, torch, 1, steps=50, warmup=5)),
             ("delta_prefill_T4096_chunked", lambda: bench_delta(lmx, torch, 4096, True)),
@@ -605,6 +646,7 @@ def main():
                                  threads=1, budget_s=10 * args.cpu_budget,
                                  what="C2 B=1 ctx 32768 decode (the headline shape)")
         cpu["all_cores"] = cpus["headline"]["all_cores"]
+        cpu["host"] = host_cpu_info()
         log(f"cpu baseline: {cpu}")
 
     line = {

@@ -24,6 +24,7 @@
 // inside every query's range skip the mask.  Workgroups are ordered so each
 // XCD owns whole kv heads (its L2 serves the G query heads that share them)
 // and heavy causal tiles start first.
+#include <algorithm>
 #include <climits>
 #include <cstdlib>
 #include <cstring>
@@ -104,9 +105,24 @@ constexpr int qk_depth() { return HD >= 512 ? 2 : (HD >= 256 ? LMX_QK_DEPTH_HD25
 // would round it twice: at Gemma's scale 1.0 with unit-RMS heads of 256 the
 // second rounding moves a score by ~2^-12 * c * sqrt(hd) ~ 6e-3 (log2
 // units, one sigma), enough to shift the output past 2e-3.
-template <int HD, int KB, int KPAD, bool EXACT>
+//
+// QLO (fp32 queries): the query row x, times c and a power of two 2^S chosen
+// per row (its largest |x c 2^S| in [2^14, 2^15)), is carried as its f16
+// rounding hi (qf) plus the f16 residual lo = f16(x c 2^S - hi), and every K
+// operand also meets lo in a second MFMA; EXACT then scales the sums by
+// 2^-S.  A score is exact to about 2^-22 of its products' sum instead of
+// 2^-12 (at scale 1.0 on RMS-normed heads, Gemma's and the vision tower's,
+// one rounding of q moves scores by ~1e-2 in log2 units).  The row scaling
+// keeps hi and the residuals of all but tiny elements in f16's normal range,
+// where they keep their full 11 bits.  ql(ks) returns the residual's fragment
+// of k-step ks (from LDS, or recomputed from the fp32 query in memory where
+// no LDS is left).
+struct NoQlo {
+    __device__ f16x8 operator()(int) const { return f16x8{}; }
+};
+template <int HD, int KB, int KPAD, bool EXACT, bool QLO = false, typename QL = NoQlo>
 __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16], f32x16 (&s)[KB], float mb,
-                                        float c, int l32, int hh) {
+                                        float c, int l32, int hh, const QL& ql = QL{}) {
     constexpr int KSTEPS = HD / 16, NQ = KSTEPS * KB;
     constexpr int D = qk_depth<HD>() < NQ ? qk_depth<HD>() : NQ;
 #pragma unroll
@@ -118,15 +134,20 @@ __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16
         return *reinterpret_cast<const f16x8*>(&Ks[(kb * 32 + l32) * KPAD + 8 * hh + ks * 16]);
     };
     f16x8 ka[NQ];
+    f16x8 qlo = {};
 #pragma unroll
     for (int q = 0; q < D; ++q) ka[q] = rd(q);
     __builtin_amdgcn_sched_group_barrier(0x100, D, 0);  // the first D reads
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
+        if constexpr (QLO) {
+            if (q % KB == 0) qlo = ql(q / KB);
+        }
         if (q + D < NQ) ka[q + D] = rd(q + D);
         s[q % KB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[q], qf[q / KB], s[q % KB], 0, 0, 0);
+        if constexpr (QLO) s[q % KB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[q], qlo, s[q % KB], 0, 0, 0);
         if (q + D < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x008, QLO ? 2 : 1, 0);        // its MFMAs
     }
     if constexpr (EXACT) {
 #pragma unroll
@@ -173,6 +194,13 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     constexpr int VPAD = BN + 4;     // Vt_s row stride (halfs), 8-byte aligned rows
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
     __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HDV * VPAD];
+    // fp32 queries: the residual of q*c after its f16 rounding, one padded row
+    // per query (the stride spreads a read's 32 rows over the banks as K_s's
+    // does); at head_dim 512 the LDS is full and it is recomputed instead.
+    constexpr bool kQlo = !kExact;
+    constexpr bool kQloLds = kQlo && HD <= 256;
+    constexpr int QLPAD = HD + 8;
+    __shared__ __attribute__((aligned(16))) f16 QL_s[kQloLds ? 4 * 32 * QLPAD : 8];
 
     // ---- which (heads, query tile, key split) this workgroup owns.  The gp
     // query heads of a workgroup share kv head kvh; each takes 4 / gp waves,
@@ -216,12 +244,33 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     const int my_hi = qvalid ? vis_hi(qpos, w, a.bidi, end) : 0;
 
     // Q as the B operand: lane holds Q[qrow][ks*16 + 8*hh + j], j < 8.  An fp32
-    // query has c = scale * log2(e) folded in before its f16 rounding (one
-    // rounding, as for Q alone); an f16 query is used as given and qk_tile
-    // scales its scores.
+    // query has c = scale * log2(e) folded in before its f16 rounding, and its
+    // residual is the second operand (kQlo); an f16 query is used as given and
+    // qk_tile scales its scores.
     f16x8 qf[KSTEPS];
+    const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
+    const float* qrow32 = reinterpret_cast<const float*>(a.q) + qoff;
+    f16* ql_row = &QL_s[kQloLds ? (wave * 32 + l32) * QLPAD + 8 * hh : 0];
+    // fp32 queries: c 2^S folded into Q (the row's largest |x c 2^S| in
+    // [2^14, 2^15); 2^S = 1 for an all-zero or non-finite row), and the
+    // scores scaled back by c_sc = 2^-S; f16 queries: Q as given, c_sc = c.
+    float qs = 1.f, c_sc = a.c;
+    if constexpr (kQlo) {
+        float m = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16);
+            const f32x4 x1 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16 + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(x0[j]), fabsf(x1[j])));
+        }
+        m = fmaxf(m, shfl_xor(m, 32)) * a.c;  // the row's two halves
+        const int S = (m > 0.f && m <= 3.402823466e38f) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+        qs = __builtin_amdgcn_ldexpf(1.f, S);
+        c_sc = __builtin_amdgcn_ldexpf(1.f, -S);
+    }
+    const float qc = a.c * qs;  // fp32 queries: x c 2^S
     {
-        const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             float x[8];
@@ -230,20 +279,61 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[j] = (float)q8[j];
             } else {
-                const float* qp = reinterpret_cast<const float*>(a.q) + qoff + ks * 16;
-                const f32x4 x0 = *reinterpret_cast<const f32x4*>(qp);
-                const f32x4 x1 = *reinterpret_cast<const f32x4*>(qp + 4);
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16 + 4);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     x[j] = x0[j];
                     x[4 + j] = x1[j];
                 }
             }
+            if constexpr (kExact) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)(kExact ? x[j] : x[j] * a.c);
+                for (int j = 0; j < 8; ++j) qf[ks][j] = (f16)x[j];
+            } else {
+                // y = x c 2^S once, and the residual taken against the very
+                // registers the MFMA reads: with contraction on, the compiler
+                // otherwise forms the residual's hi as one fused
+                // multiply-convert (one rounding) and the MFMA operand's as
+                // multiply then convert (two), which differ by an f16 ulp
+                // where the fp32 product is a tie.
+                float y[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    y[j] = x[j] * qc;
+                    asm volatile("" : "+v"(y[j]));
+                    qf[ks][j] = (f16)y[j];
+                }
+                asm volatile("" : "+v"(qf[ks]));
+                if constexpr (kQloLds) {
+                    f16x8 lo;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) lo[j] = (f16)(y[j] - (float)qf[ks][j]);
+                    *reinterpret_cast<f16x8*>(ql_row + ks * 16) = lo;
+                }
+            }
         }
         settle_q(qf);
     }
+    // The residual's fragment of k-step ks (read after the first barrier of
+    // the key loop, which orders the stores above before it).
+    auto ql = [&](int ks) -> f16x8 {
+        if constexpr (kQloLds) {
+            return *reinterpret_cast<const f16x8*>(ql_row + ks * 16);
+        } else if constexpr (kQlo) {
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16);
+            const f32x4 x1 = *reinterpret_cast<const f32x4*>(qrow32 + ks * 16 + 4);
+            f16x8 lo;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo[j] = (f16)(x0[j] * qc - (float)qf[ks][j]);
+                lo[4 + j] = (f16)(x1[j] * qc - (float)qf[ks][4 + j]);
+            }
+            return lo;
+        } else {
+            return f16x8{};
+        }
+    };
 
     // ---- key ranges: the workgroup's, and this wave's
     const int q_last = min(q0 + bm, t) - 1;
@@ -404,7 +494,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         //      come out already shifted for exp2.
         float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
-        qk_tile<HD, KB, KPAD, kExact>(Ks, qf, s, mb, a.c, l32, hh);
+        qk_tile<HD, KB, KPAD, true, kQlo>(Ks, qf, s, mb, c_sc, l32, hh, ql);
 
         // ---- mask, online softmax.  s[kb][i] is key
         //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
@@ -1295,18 +1385,20 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
 // per CU: it pays when there are at least two workgroups per CU (S >= 4096 at
 // 32 heads; at S = 2048 a single round of unequal causal workgroups leaves
 // CUs idle, and the 128-row kernel is faster).  LMX_PREFILL_KERNEL=pp|tile
-// forces one of them (tuning overrides, for tests and sweeps).
-static bool use_ping_pong(int hd, long n_tokens, long n_heads) {
-    if (hd != 128) return false;
+// forces one of them (tuning overrides, for tests and sweeps).  fp32 queries
+// take the 128-row kernel, which carries their f16 residual (qk_tile).
+static bool use_ping_pong(int hd, long n_tokens, long n_heads, lmx_dtype q_dt) {
+    if (hd != 128 || q_dt != LMX_F16) return false;
     if (const int f = tuning().prefill_kernel; f >= 0) return f == 1;
     return (n_tokens + kPpBM - 1) / kPpBM * n_heads >= 512;
 }
 
 // Query heads per prefill workgroup (they share one kv head).  At head_dim
 // >= 256 two heads of a kv group share a workgroup (64 rows each): a
-// 1024-key window then spans 34 key tiles per workgroup instead of 36, at
-// the same MFMA work per tile.  LMX_PREFILL_GP=1|2|4 overrides it (tuning
-// overrides, for tests and sweeps) where it divides G.
+// 1024-key window then spans fewer key tiles per workgroup at the same MFMA
+// work per tile.
+// LMX_PREFILL_GP=1|2|4 overrides it (tuning overrides, for tests and sweeps)
+// where it divides G.
 static int prefill_gp(int hd, int G, bool pp) {
     if (const int v = tuning().prefill_gp; v > 0 && G % v == 0) return v;
     if (pp) return 1;
@@ -1322,9 +1414,9 @@ constexpr int kMinSplitTiles = 8;
 constexpr int kMaxSplits = 16;
 constexpr int kCus = 256;
 int decode_max_vis(const lmx_attn_params* p);
-static int prefill_splits(const lmx_attn_params* p) {
+static int prefill_splits(const lmx_attn_params* p, lmx_dtype q_dt) {
     const int hd = (int)p->head_dim;
-    if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads)) return 1;
+    if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads, q_dt)) return 1;
     const int gp = prefill_gp(hd, (int)(p->n_heads / p->n_kv_heads), false);
     const long bm = kPfBM / gp;
     const long n_wg = (long)((p->n_tokens + bm - 1) / bm) * (p->n_heads / gp) * (hd >= 512 ? 2 : 1);
@@ -1343,7 +1435,7 @@ static int prefill_splits(const lmx_attn_params* p) {
 static size_t round_up256(size_t x) { return (x + 255) / 256 * 256; }
 
 size_t prefill_workspace_bytes(const lmx_attn_params* p) {
-    const int sp = prefill_splits(p);
+    const int sp = std::max(prefill_splits(p, LMX_F16), prefill_splits(p, LMX_F32));
     if (sp == 1) return 0;
     const size_t rows = (size_t)sp * p->n_tokens * p->n_heads;
     return round_up256(rows * 2 * sizeof(float)) + round_up256(rows * p->head_dim * sizeof(float));
@@ -1358,7 +1450,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
                        const void* k_cache, const void* v_cache, const void* k_cur, const void* v_cur,
                        float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     PrefillArgs a{};
-    a.n_split = prefill_splits(p);
+    a.n_split = prefill_splits(p, q_dt);
     if (a.n_split > 1) {
         if (!ws || ws_bytes < prefill_workspace_bytes(p)) return LMX_E_WORKSPACE;
         if (((uintptr_t)ws & 255) != 0) return LMX_E_ALIGN;
@@ -1386,7 +1478,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     a.c = p->scale * kLog2e;
     window_magic((uint32_t)a.window, &a.w_magic, &a.w_shift);
     const int hd = (int)p->head_dim;
-    const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads);
+    const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads, q_dt);
     a.gp = prefill_gp(hd, a.G, pp);
     const int bm = (pp ? kPpBM : kPfBM) / a.gp;
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
@@ -1404,7 +1496,7 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     // grid would fill at most half the CUs.  LMX_PREFILL_KH=0 turns it off
     // (tuning overrides, for tests and A/B timing).
     const bool kh = !pp && hd <= 128 && lin && a.n_split == 1 && a.gp == 1 && 2 * nblk <= kPfCus &&
-                    tuning().prefill_kh != 0;
+                    q_dt == LMX_F16 && tuning().prefill_kh != 0;
     if (kh) {
         a.n_qtiles = (a.n_tokens + 63) / 64;
         nblk = (long)a.n_qtiles * a.H;
@@ -1422,20 +1514,11 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
         if (lin) hipLaunchKernelGGL((attn_prefill_pp_kernel<QT, 128, true>), grid, dim3(512), 0, st, a); \
         else hipLaunchKernelGGL((attn_prefill_pp_kernel<QT, 128, false>), grid, dim3(512), 0, st, a);   \
     } while (0)
-    if (kh) {
-        const bool f16q = q_dt == LMX_F16;
-        if (hd == 64) {
-            if (f16q) hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 64>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((attn_prefill_kh_kernel<float, 64>), grid, dim3(256), 0, st, a);
-        } else {
-            if (f16q) hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 128>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((attn_prefill_kh_kernel<float, 128>), grid, dim3(256), 0, st, a);
-        }
-    } else if (pp) {
-        if (q_dt == LMX_F16)
-            LMX_PP(f16);
-        else
-            LMX_PP(float);
+    if (kh) {  // f16 queries only
+        if (hd == 64) hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 64>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((attn_prefill_kh_kernel<f16, 128>), grid, dim3(256), 0, st, a);
+    } else if (pp) {  // f16 queries only
+        LMX_PP(f16);
     } else if (q_dt == LMX_F16) {
         if (hd == 64) LMX_PF(f16, 64);
         else if (hd == 128) LMX_PF(f16, 128);

@@ -298,11 +298,15 @@ def test_exact_check_rejects_a_planted_off_by_one():
     (128, 32, 8, 1024, 0, 0),       # both kernels at hd 128
     (512, 16, 1, 1024, 0, 0),       # Gemma 4 global layer shape
 ])
-def test_scale_one_qk_normed_prefill(hd, H, Hkv, t, base, window, prefill_kernel):
-    say(f"scale 1.0 prefill[{prefill_kernel}] hd={hd} t={t} base={base} w={window}")
-    c = AttnCase(hd + t + base + window, t=t, H=H, Hkv=Hkv, hd=hd, n_pos=base + t, q_f16=True,
+@pytest.mark.parametrize("q_f16", [True, False])
+def test_scale_one_qk_normed_prefill(hd, H, Hkv, t, base, window, q_f16, prefill_kernel):
+    # f16 queries enter the MFMA as given; fp32 queries as their f16 rounding
+    # plus its f16 residual (one rounding alone moves scale-1.0 scores by
+    # ~1e-2 in log2 units, past the tolerance)
+    say(f"scale 1.0 prefill[{prefill_kernel}] hd={hd} t={t} base={base} w={window} q_f16={q_f16}")
+    c = AttnCase(hd + t + base + window, t=t, H=H, Hkv=Hkv, hd=hd, n_pos=base + t, q_f16=q_f16,
                  qk_norm=True)
-    q = dev(c.q.astype(np.float16))
+    q = dev(c.q.astype(np.float16)) if q_f16 else dev(c.q)
     if window:
         ring = np.zeros((window, c.kv_dim), np.uint16)
         for p in range(max(0, base - window), base):
@@ -318,7 +322,10 @@ def test_scale_one_qk_normed_prefill(hd, H, Hkv, t, base, window, prefill_kernel
                             n_kv_heads=Hkv, head_dim=hd, base_pos=base, scale=1.0)
     torch.cuda.synchronize()
     ref = c.reference(base_pos=base, window=window, scale=1.0, threads=ORACLE_THREADS)
-    e = assert_close(out.cpu().numpy(), ref, what="scale 1.0 prefill")
+    # fp32 queries at a tighter bound: their error is the f16 P rounding
+    # alone (about 5e-4 here, as for f16 queries against their own oracle);
+    # a residual taken against a differently rounded hi showed as 2.6e-3
+    e = assert_close(out.cpu().numpy(), ref, abs_tol=2e-3 if q_f16 else 1.5e-3, what="scale 1.0 prefill")
     say(f"  max_abs={e[0]:.2e} rel={e[1]:.2e}")
 
 

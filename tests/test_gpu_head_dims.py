@@ -69,6 +69,14 @@ def test_decode_odd_sizes(hd):
     run(c, base=299)
 
 
+@pytest.mark.parametrize("hd", [72, 80, 96])
+def test_vision_bidi_prefill_scale_one(hd):
+    # the vision tower's call: H = Hkv, bidirectional, scale 1.0, RMS-normed
+    # q and k (its rms_norm before attention)
+    c = AttnCase(hd + 7, t=300, H=8, Hkv=8, hd=hd, n_pos=300, qk_norm=True)
+    run(c, base=0, bidi=True, scale=1.0)
+
+
 @pytest.mark.parametrize("hd", [72, 120])
 def test_causal_prefill_with_history(hd):
     c = AttnCase(hd + 11, t=150, H=12, Hkv=4, hd=hd, n_pos=150 + 333, q_f16=True, qk_norm=True)
