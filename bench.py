@@ -591,8 +591,7 @@ def main():
                                                               warmup=1)),
             # Gemma 4's real global layers: hd 512, one kv head, scale 1.0 on
             # RMS-normed q and k (ARCHITECTURE.md:25-28, 54-62); FLOPs are the
-            # algorithmic 4*hd*H per visible pair, not the 1.5x the two
-            # output-dim workgroups of a (head, tile) issue
+            # algorithmic 4*hd*H per visible pair
             ("gemma4_global_prefill_4k_hd512", lambda: bench_prefill(lmx, torch, 4096, Hq=16, Hkv=1, hd=512,
                                                                      scale=1.0, qk_norm=True, steps=5,
                                                                      warmup=1)),

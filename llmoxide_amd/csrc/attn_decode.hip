@@ -8,9 +8,17 @@ namespace lmx {
 
 // Query heads per wave: the largest divisor of G within the register budget
 // (o holds gb * hd/16 floats per lane, K/V tiles grow with hd) and the 16
-// MFMA columns (an fp32 query takes two columns per head).
+// MFMA columns (an fp32 query takes two columns per head).  Each head block
+// (G / gb of them per kv head) streams the kv head's rows again; at head_dim
+// 512 four heads a wave still fit (256 VGPRs + 64 AGPRs, no spills): Gemma 4's
+// global layers (16 query heads on one kv head, 32k keys) went from 102 us a
+// call at gb 1 to 42 us at gb 4 (55 at gb 2), with the K/V loads cached
+// (LMX_DEC_SHARED_HD) so that the XCD's L2 serves part of the repeats.
+#ifndef LMX_DEC_GB512
+#define LMX_DEC_GB512 4
+#endif
 static int pick_gb(int G, int hd) {
-    const int cap = hd >= 512 ? 1 : (hd == 256 ? 2 : (hd == 128 ? 6 : 8));
+    const int cap = hd >= 512 ? LMX_DEC_GB512 : (hd == 256 ? 2 : (hd == 128 ? 6 : 8));
     for (int gb = cap; gb >= 1; --gb)
         if (G % gb == 0) return gb;
     return 1;

@@ -101,6 +101,9 @@ constexpr int kMergePer = 8;            // partials per merge thread
 #ifndef LMX_DEC_DEPTH_256
 #define LMX_DEC_DEPTH_256 1  // at head_dim 256
 #endif
+#ifndef LMX_DEC_SHARED_HD
+#define LMX_DEC_SHARED_HD 512  // head sizes from this one up load K/V through L2
+#endif
 
 // Visible keys [lo, hi] of query row qi (attn.wgsl:52-66 first/last_visible;
 // batched: the sequence's last position).
@@ -158,12 +161,18 @@ __device__ __forceinline__ int v_dim(int c16, int r, int j) {
     return HD >= 128 ? 128 * r + 8 * c16 + j : 4 * c16 + j;
 }
 
-// Streaming loads: the cache is read once per call.
+// Streaming loads where the cache is read once per call (NT); plain loads
+// where several head blocks of one kv head read the same rows, so that the
+// XCD's L2 serves all but the first.
+template <bool NT>
 __device__ __forceinline__ f16x8 ld_stream8(const f16* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+    return *reinterpret_cast<const f16x8*>(p);
 }
+template <bool NT>
 __device__ __forceinline__ f16x4 ld_stream4(const f16* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
+    return *reinterpret_cast<const f16x4*>(p);
 }
 
 // Merge: thread (column, part) folds partials part, part + m_parts, ... (at
@@ -256,6 +265,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     constexpr int DPL = HD / 16;  // V dims per lane
     constexpr int WPH = kWaves / HW;  // waves per kv head
     constexpr bool SPLIT_Q = sizeof(QT) == 4;
+    constexpr bool kNtLoads = HD < LMX_DEC_SHARED_HD;
     // PIPE also at head_dim 256 with DEPTH 1: the first tile's loads go out
     // with the query's, before its conversion (Gemma global decode 43.6 ->
     // 41.6 us, the 1024-key window 0.6 us shorter per workgroup).
@@ -334,12 +344,12 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
             for (int i = 0; i < 4; ++i) {
                 const f16* krow = row_ptr(kc, a.k_cur, min(kt + 4 * g4 + i, hi));
 #pragma unroll
-                for (int r = 0; r < KRP; ++r) b.k[i * KRP + r] = ld_stream8(krow + 128 * r + 8 * c16);
+                for (int r = 0; r < KRP; ++r) b.k[i * KRP + r] = ld_stream8<kNtLoads>(krow + 128 * r + 8 * c16);
             }
         } else {
             const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi));
 #pragma unroll
-            for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8(krow + 32 * s + 8 * g4);
+            for (int s = 0; s < KS; ++s) b.k[s] = ld_stream8<kNtLoads>(krow + 32 * s + 8 * g4);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -348,11 +358,11 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
             for (int r = 0; r < VR; ++r) {
                 const f16* vp = vrow + v_dim<HD>(c16, r, 0);
                 if constexpr (VW == 8) {
-                    const f16x8 x = ld_stream8(vp);
+                    const f16x8 x = ld_stream8<kNtLoads>(vp);
                     b.v[i][r].v[0] = f16x4{x[0], x[1], x[2], x[3]};
                     b.v[i][r].v[1] = f16x4{x[4], x[5], x[6], x[7]};
                 } else {
-                    b.v[i][r].v[0] = ld_stream4(vp);
+                    b.v[i][r].v[0] = ld_stream4<kNtLoads>(vp);
                 }
             }
         }
@@ -719,7 +729,7 @@ inline lmx_status launch_decode_hw(const DecodeArgs& a, int hd, int gb, bool kro
     LMX_DEC_CASE(128, 1) LMX_DEC_CASE(128, 2) LMX_DEC_CASE(128, 3) LMX_DEC_CASE(128, 4)
     LMX_DEC_CASE(128, 5) LMX_DEC_CASE(128, 6)
     LMX_DEC_CASE(256, 1) LMX_DEC_CASE(256, 2)
-    LMX_DEC_CASE(512, 1)
+    LMX_DEC_CASE(512, 1) LMX_DEC_CASE(512, 2) LMX_DEC_CASE(512, 4)
 #undef LMX_DEC_CASE
     return LMX_E_UNSUPPORTED;
 }

@@ -65,13 +65,15 @@ constexpr int kPfCus = 256;  // compute units of the target (MI355X)
 // the next tile and the o accumulators share one register file).
 template <int HD>
 constexpr int pf_bn() { return HD >= 256 ? 32 : 64; }
-// Output dim slices: at head_dim 512 a wave cannot hold Q and a 32 x 512
-// fp32 output block in registers, so two workgroups share a (head, query
-// tile): each forms the whole S = Q K^T (the same scores and softmax in
-// both) and accumulates P V for its half of the dims, staging only that half
-// of V (1.5x the MFMA work of one pass, the register budget of head_dim 256).
+// Wave pairs at head_dim 512: a wave cannot hold a 32-row block's Q and its
+// 32 x 512 fp32 output in registers, so two waves share each block, one per
+// half of the head's dims.  Each holds its half of Q and of the output (the
+// register budget of head_dim 256), forms the partial S over its 256 dims,
+// and the two partials are summed through LDS; both waves then hold the
+// same scores (a + b = b + a in IEEE arithmetic), run the same softmax, and
+// accumulate P V for their own half.  The MFMA work is that of one pass.
 template <int HD>
-constexpr int pf_dslices() { return HD >= 512 ? 2 : 1; }
+constexpr bool pf_pair() { return HD >= 512; }
 constexpr float kRescaleSlack = 8.f;  // log2 units a running max may lag by
 
 // attn.wgsl:52-66
@@ -97,6 +99,16 @@ __device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
 #endif
 template <int HD>
 constexpr int qk_depth() { return HD >= 512 ? 2 : (HD >= 256 ? LMX_QK_DEPTH_HD256 : 4); }
+// The wave pairs of head_dim 512 hold twice the K/V prefetch of head_dim 256
+// in registers: shallower operand rings keep them out of scratch.
+#ifndef LMX_PAIR_QK_DEPTH
+#define LMX_PAIR_QK_DEPTH 2
+#endif
+#ifndef LMX_PAIR_PV_DEPTH
+#define LMX_PAIR_PV_DEPTH 1
+#endif
+constexpr int kPairQkDepth = LMX_PAIR_QK_DEPTH;
+constexpr int kPairPvDepth = LMX_PAIR_PV_DEPTH;
 //
 // EXACT: Q holds the caller's f16 values and the scores are scaled by
 // c = scale * log2(e) in fp32 after the MFMAs (one FMA per score).  Else c
@@ -120,11 +132,11 @@ constexpr int qk_depth() { return HD >= 512 ? 2 : (HD >= 256 ? LMX_QK_DEPTH_HD25
 struct NoQlo {
     __device__ f16x8 operator()(int) const { return f16x8{}; }
 };
-template <int HD, int KB, int KPAD, bool EXACT, bool QLO = false, typename QL = NoQlo>
+template <int HD, int KB, int KPAD, bool EXACT, bool QLO = false, typename QL = NoQlo, int DEP = qk_depth<HD>()>
 __device__ __forceinline__ void qk_tile(const f16* Ks, const f16x8 (&qf)[HD / 16], f32x16 (&s)[KB], float mb,
                                         float c, int l32, int hh, const QL& ql = QL{}) {
     constexpr int KSTEPS = HD / 16, NQ = KSTEPS * KB;
-    constexpr int D = qk_depth<HD>() < NQ ? qk_depth<HD>() : NQ;
+    constexpr int D = DEP < NQ ? DEP : NQ;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -171,6 +183,19 @@ __device__ __forceinline__ void settle_q(f16x8 (&qf)[N]) {
 // (inline assembly it does not): every load issued before it is complete.
 __device__ __forceinline__ void drain_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// A raw buffer resource over p (dword 3 = 0x00020000: 32-bit data format, the
+// form raw buffer loads take on gfx9 parts) with 2^31 - 1 bytes of range,
+// which the rows of one K/V tile never leave.  p must be wave-uniform: it is
+// moved to scalar registers first (readfirstlane), since a resource built in
+// vector registers makes the compiler wrap every load in a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    void* q = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(q, 0, 0x7fffffff, 0x00020000);
+}
+
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
     const int q = n / 8, r = n % 8;
     const int xcd = bid % 8, local = bid / 8;
@@ -184,16 +209,20 @@ template <typename QT, int HD, bool LIN>
 __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(PrefillArgs a) {
     constexpr bool kExact = sizeof(QT) == 2;  // f16 queries: scale applied in fp32 (qk_tile)
     constexpr int BN = pf_bn<HD>();
-    constexpr int DS = pf_dslices<HD>();  // output dim slices, one per workgroup
-    constexpr int HDV = HD / DS;     // V / output dims of this workgroup
+    constexpr bool kPair = pf_pair<HD>();
+    constexpr int QD = kPair ? HD / 2 : HD;  // Q dims a wave holds (its half, kPair)
+    constexpr int HDV = QD;          // output dims a wave accumulates
     constexpr int KB = BN / 32;      // 32-key MFMA blocks per tile
     constexpr int PST = BN / 16;     // 16-key P.V k-steps per tile
-    constexpr int KSTEPS = HD / 16;  // MFMA k-steps over head_dim
+    constexpr int KSTEPS = QD / 16;  // MFMA k-steps over the wave's dims
     constexpr int NB = HDV / 32;     // 32-dim output blocks
     constexpr int KPAD = HD + 8;     // K_s row stride (halfs)
     constexpr int VPAD = BN + 4;     // Vt_s row stride (halfs), 8-byte aligned rows
     __shared__ __attribute__((aligned(16))) f16 K_s[2 * BN * KPAD];   // two stages
-    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HDV * VPAD];
+    __shared__ __attribute__((aligned(16))) f16 Vt_s[2 * HD * VPAD];
+    // kPair: each wave's partial scores, 16 floats a lane as four f32x4
+    // planes of 64 lanes (conflict-free 16-byte accesses)
+    __shared__ __attribute__((aligned(16))) float X_s[kPair ? 4 * 16 * 64 : 4];
     // fp32 queries: the residual of q*c after its f16 rounding, one padded row
     // per query (the stride spreads a read's 32 rows over the banks as K_s's
     // does); at head_dim 512 the LDS is full and it is recomputed instead.
@@ -211,30 +240,37 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     const int logical = xcd_remap(blockIdx.x, nblk);
     const int n_split = a.n_split;
     const int gp = a.gp, hgroups = a.G / gp;
-    const int per_kvh = a.n_qtiles * hgroups * n_split * DS;
+    const int per_kvh = a.n_qtiles * hgroups * n_split;
     const int kvh = logical / per_kvh;
     const int rem = logical - kvh * per_kvh;
     // Query tiles heaviest first (causal work grows with qt).  When the whole
     // grid is resident at once (two workgroups per CU), the second half is
     // walked lightest first, so the two workgroups a CU receives pair a heavy
     // tile with a light one instead of two of nearly the same weight.
-    const int pos = rem / (hgroups * n_split * DS);
+    const int pos = rem / (hgroups * n_split);
     const int half = (a.n_qtiles + 1) / 2;
     const bool fold = HD <= 128 && nblk <= 2 * kPfCus;
     const int qt = (fold && pos >= half) ? pos - half : a.n_qtiles - 1 - pos;
-    const int rem2 = rem % (hgroups * n_split * DS);
-    const int sp = (rem2 % (n_split * DS)) / DS;
-    const int ds = rem2 % DS;  // this workgroup's output dims: [ds * HDV, + HDV)
+    const int rem2 = rem % (hgroups * n_split);
+    const int sp = rem2 % n_split;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave: uniform by construction (readfirstlane), so the branches and loop
+    // bounds it feeds are wave-uniform to the compiler too, and the tile
+    // pointers derived from them stay scalar (no waterfall loops around
+    // buffer loads)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hh = lane >> 5;
-    const int wph = 4 / gp;             // waves per query head
-    const int bm = kPfBM / gp;          // query rows per head
-    const int h = kvh * a.G + (rem2 / (n_split * DS)) * gp + wave / wph;  // this wave's head
+    // kPair: waves w and w ^ 2 share a 32-row block, dims [dh * QD, + QD)
+    // each; otherwise every wave has its own block of all the dims.
+    const int dh = kPair ? wave >> 1 : 0;
+    const int wr = kPair ? wave & 1 : wave;  // the wave's row block
+    const int wph = (kPair ? 2 : 4) / gp;    // row blocks per query head
+    const int bm = 32 * wph;                 // query rows per head
+    const int h = kvh * a.G + (rem2 / n_split) * gp + wr / wph;  // this wave's head
     const int t = a.n_tokens, base = a.base_pos, w = a.window;
     const int end = base + t - 1;
     const int q0 = qt * bm;
-    const int qw0 = q0 + (wave % wph) * 32;
+    const int qw0 = q0 + (wr % wph) * 32;
 
     // ---- this lane's query (column l32 of the wave's S^T tiles)
     const int qrow = qw0 + l32;
@@ -248,7 +284,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     // residual is the second operand (kQlo); an f16 query is used as given and
     // qk_tile scales its scores.
     f16x8 qf[KSTEPS];
-    const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + 8 * hh;
+    const size_t qoff = ((size_t)(qvalid ? qrow : 0) * a.H + h) * a.q_stride + dh * QD + 8 * hh;
     const float* qrow32 = reinterpret_cast<const float*>(a.q) + qoff;
     f16* ql_row = &QL_s[kQloLds ? (wave * 32 + l32) * QLPAD + 8 * hh : 0];
     // fp32 queries: c 2^S folded into Q (the row's largest |x c 2^S| in
@@ -363,12 +399,20 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
     // banks once.  Consecutive dims would put lanes 8 rows apart, on two
     // banks (the row stride is 16 banks mod 32).
     constexpr int KCH = HD / 8;                   // 16-byte chunks per key row
-    constexpr int KCHV = HDV / 8;                 // 16-byte chunks of a V row slice
+    constexpr int KCHV = HD / 8;                  // 16-byte chunks of a V row
     constexpr int KPT = BN * KCH / 256;           // K chunks per thread
     constexpr int VPT = (KCHV * (BN / 4) + 255) / 256;  // V 4-key groups per thread
     static_assert(BN * KCH % 256 == 0, "K tile split");
     f16x8 rk[KPT];
     f16x8 rv[VPT][4];
+    // kBufFetch: the fast path's per-thread byte offsets from a tile's first
+    // row (thread tid takes K chunk tid % KCH of row tid / KCH, and V dims
+    // 8 (tid / (BN / 4)) of rows 4 (tid % (BN / 4)) + u; each later load adds
+    // a whole number of rows or chunks)
+    constexpr bool kBufFetch = true;
+    static_assert(256 % KCH == 0 && 256 % (BN / 4) == 0, "uniform load strides");
+    const int k_voff = (tid / KCH) * a.kv_dim * 2 + (tid % KCH) * 16;
+    const int v_voff = 4 * (tid % (BN / 4)) * a.kv_dim * 2 + (tid / (BN / 4)) * 16;
     // Row of position p: a k_cur row for p >= cur_begin, else cache slot
     // p % w (a multiply-high, not a division).
     auto row_src = [&](const f16* cache, const f16* cur, int p) -> const f16* {
@@ -401,7 +445,28 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             vb = a.v + (size_t)s0 * a.kv_dim;
         }
         kb += kvh * HD;
-        vb += kvh * HD + ds * HDV;
+        vb += kvh * HD;
+        if constexpr (kBufFetch) {
+            // Buffer loads from the tile's first row: the per-load strides go
+            // in the scalar offset and the immediate, so a thread keeps one
+            // 32-bit offset for K and one for V, not a 64-bit address a load.
+            const int kvb = a.kv_dim * 2;  // bytes per row
+            const __amdgpu_buffer_rsrc_t rk_src = make_rsrc(kb), rv_src = make_rsrc(vb);
+#pragma unroll
+            for (int i = 0; i < KPT; ++i)
+                rk[i] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk_src, k_voff, i * (256 / KCH) * kvb, 0));
+#pragma unroll
+            for (int i = 0; i < VPT; ++i) {
+                if (tid + 256 * i < KCHV * (BN / 4))
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        rv[i][u] = __builtin_bit_cast(
+                            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv_src, v_voff + i * (256 / (BN / 4)) * 16,
+                                                                          u * kvb, 0));
+            }
+            return true;
+        }
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + 256 * i;
@@ -443,15 +508,14 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
                 const int p = kt + 4 * kg + u;
                 f16x8 val = {};
                 if (pr < KCHV * (BN / 4) && p >= wg_lo && p <= wg_hi)
-                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + ds * HDV +
-                                                          dc * 8);
+                    val = *reinterpret_cast<const f16x8*>(row_src(a.v, a.v_cur, p) + kvh * HD + dc * 8);
                 rv[i][u] = val;
             }
         }
     };
     auto stash = [&](int stage) {
         f16* Ks = K_s + stage * (BN * KPAD);
-        f16* Vts = Vt_s + stage * (HDV * VPAD);
+        f16* Vts = Vt_s + stage * (HD * VPAD);
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + 256 * i;
@@ -484,17 +548,41 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         stash(stage);
         __syncthreads();
         if (kt + BN <= kt_stop) fetch(kt + BN);
-        if (!wave_live || kt > wv_hi || kt + BN - 1 < wv_lo) continue;  // wave-uniform
+        // wave-uniform, and the same for both waves of a kPair block
+        const bool live = wave_live && kt <= wv_hi && kt + BN - 1 >= wv_lo;
+        if (!kPair && !live) continue;
         const bool need_mask = !(kt >= wv_lo_max && kt + BN - 1 <= wv_hi_min);
         const f16* Ks = K_s + stage * (BN * KPAD);
-        const f16* Vts = Vt_s + stage * (HDV * VPAD);
+        const f16* Vts = Vt_s + stage * (HD * VPAD) + dh * HDV * VPAD;
 
         // ---- S^T - m = K Q^T - m, two 32-key blocks.  The accumulators start
         //      at -mb (mb = the running max once one is set), so the scores
-        //      come out already shifted for exp2.
+        //      come out already shifted for exp2.  kPair: each wave's partial
+        //      over its dims, scaled (c_sc), goes through X_s; every wave
+        //      meets the barrier, live or not; the sum is then shifted by mb.
         float mb = m_run > -1e29f ? m_run : 0.f;
         f32x16 s[KB];
-        qk_tile<HD, KB, KPAD, true, kQlo>(Ks, qf, s, mb, c_sc, l32, hh, ql);
+        if constexpr (kPair) {
+            static_assert(KB == 1, "one 32-key block per tile in the pair exchange");
+            if (live) {
+                qk_tile<QD, KB, KPAD, true, kQlo, decltype(ql), kPairQkDepth>(Ks + dh * QD, qf, s, 0.f, c_sc, l32,
+                                                                              hh, ql);
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<f32x4*>(&X_s[((wave * 4 + g) * 64 + lane) * 4]) =
+                        f32x4{s[0][4 * g], s[0][4 * g + 1], s[0][4 * g + 2], s[0][4 * g + 3]};
+            }
+            __syncthreads();
+            if (!live) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 o4 = *reinterpret_cast<const f32x4*>(&X_s[(((wave ^ 2) * 4 + g) * 64 + lane) * 4]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[0][4 * g + j] = (s[0][4 * g + j] + o4[j]) - mb;
+            }
+        } else {
+            qk_tile<HD, KB, KPAD, true, kQlo>(Ks, qf, s, mb, c_sc, l32, hh, ql);
+        }
 
         // ---- mask, online softmax.  s[kb][i] is key
         //      kt + 32*kb + 8*(i/4) + 4*hh + i%4 for query qrow, minus mb.
@@ -586,7 +674,7 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
             // Operands PVD blocks ahead: 2 at head_dim >= 256, where one wave
             // per SIMD waits out each LDS round trip (+1.2% on Gemma's 4k
             // prefill; 3 measured the same), 1 below.
-            constexpr int PVD = HD >= 256 ? 2 : 1;
+            constexpr int PVD = kPair ? kPairPvDepth : (HD >= 256 ? 2 : 1);
             static_assert(PVD < NB, "operand ring");
             f16x8 va[PVD + 1][2];
 #pragma unroll
@@ -611,8 +699,8 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         // the split's partial: o as accumulated, and (m, l); an empty split
         // leaves m = -1e30, l = 0, o = 0
         const size_t row = ((size_t)sp * t + qrow) * a.H + h;
-        if (hh == 0 && ds == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * row) = f32x2{m_run, l_tot};
-        float* prow = a.part_o + row * HD + ds * HDV;
+        if (hh == 0 && dh == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * row) = f32x2{m_run, l_tot};
+        float* prow = a.part_o + row * HD + dh * HDV;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -622,8 +710,8 @@ __global__ __launch_bounds__(256, HD > 128 ? 1 : 2) void attn_prefill_kernel(Pre
         return;
     }
     const float inv = 1.f / l_tot;
-    float* orow = a.out + ((size_t)qrow * a.H + h) * HD + ds * HDV;
-    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride + ds * HDV : nullptr;
+    float* orow = a.out + ((size_t)qrow * a.H + h) * HD + dh * HDV;
+    const float* grow = a.gate ? a.gate + ((size_t)qrow * a.H + h) * a.gate_stride + dh * HDV : nullptr;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -1394,16 +1482,20 @@ static bool use_ping_pong(int hd, long n_tokens, long n_heads, lmx_dtype q_dt) {
 }
 
 // Query heads per prefill workgroup (they share one kv head).  At head_dim
-// >= 256 two heads of a kv group share a workgroup (64 rows each): a
-// 1024-key window then spans fewer key tiles per workgroup at the same MFMA
-// work per tile.
+// 256 two heads of a kv group share a workgroup (64 rows each): a 1024-key
+// window then spans fewer key tiles per workgroup at the same MFMA work per
+// tile.  At head_dim 512 (wave pairs, two 32-row blocks a workgroup) one.
 // LMX_PREFILL_GP=1|2|4 overrides it (tuning overrides, for tests and sweeps)
-// where it divides G.
+// where it divides G and the workgroup has that many row blocks.
 static int prefill_gp(int hd, int G, bool pp) {
-    if (const int v = tuning().prefill_gp; v > 0 && G % v == 0) return v;
-    if (pp) return 1;
+    const int blocks = hd >= 512 ? 2 : 4;
+    if (const int v = tuning().prefill_gp; v > 0 && G % v == 0 && v <= blocks) return v;
+    if (pp || hd >= 512) return 1;
     return hd >= 256 && G % 2 == 0 ? 2 : 1;
 }
+
+// Query rows per attn_prefill_kernel workgroup and head: 32 per row block.
+static int prefill_rows(int hd, int gp) { return (hd >= 512 ? kPfBM / 2 : kPfBM) / gp; }
 
 // Key splits for attn_prefill_kernel.  When the query tiles give fewer
 // workgroups than the CUs hold at once (two per CU, one at head_dim 256), as
@@ -1418,8 +1510,8 @@ static int prefill_splits(const lmx_attn_params* p, lmx_dtype q_dt) {
     const int hd = (int)p->head_dim;
     if (use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads, q_dt)) return 1;
     const int gp = prefill_gp(hd, (int)(p->n_heads / p->n_kv_heads), false);
-    const long bm = kPfBM / gp;
-    const long n_wg = (long)((p->n_tokens + bm - 1) / bm) * (p->n_heads / gp) * (hd >= 512 ? 2 : 1);
+    const long bm = prefill_rows(hd, gp);
+    const long n_wg = (long)((p->n_tokens + bm - 1) / bm) * (p->n_heads / gp);
     const long slots = (long)kCus * (hd > 128 ? 1 : 2);
     if (n_wg >= slots) return 1;
     const int bn = hd >= 256 ? 32 : 64;
@@ -1480,9 +1572,9 @@ lmx_status prefill_fwd(const lmx_attn_params* p, const AttnIo& io, const void* q
     const int hd = (int)p->head_dim;
     const bool pp = use_ping_pong(hd, (long)p->n_tokens, (long)p->n_heads, q_dt);
     a.gp = prefill_gp(hd, a.G, pp);
-    const int bm = (pp ? kPpBM : kPfBM) / a.gp;
+    const int bm = pp ? kPpBM / a.gp : prefill_rows(hd, a.gp);
     a.n_qtiles = (a.n_tokens + bm - 1) / bm;
-    long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split * (pp ? 1 : (hd >= 512 ? 2 : 1));
+    long nblk = (long)a.n_qtiles * (a.H / a.gp) * a.n_split;
     // Linear addressing: no k_cur rows and every position below the window;
     // or a batch at base 0 whose every key is a k_cur row (row p of k_cur is
     // position p), as a first windowed prefill chunk is.
