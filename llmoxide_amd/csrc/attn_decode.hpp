@@ -63,6 +63,14 @@ namespace lmx {
 
 enum DecodeMode { kModeLinear = 0, kModeGeneral = 1, kModeBatched = 2 };
 
+// Timeline hook: a measurement build defines LMX_DECODE_MARK(i) before
+// including this header (llmoxide_amd/timeline/decode_timeline.hip stores each
+// wave's s_memrealtime at phase i: 0 entry, 1 query converted, 2 first tile
+// done, 3 last tile done, 4 partials stored).  The library leaves it empty.
+#ifndef LMX_DECODE_MARK
+#define LMX_DECODE_MARK(i) ((void)0)
+#endif
+
 struct DecodeArgs {
     const void* q;
     const f16* k;
@@ -284,6 +292,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         args_in_sgprs(a.k_ptrs, a.v_ptrs, a.ctx_lens, a.max_ctx);
     else
         args_in_sgprs(a.k, a.v, a.k_cur, a.v_cur, a.base_pos, a.n_tokens, a.bidi, a.w_magic, a.w_shift);
+    LMX_DECODE_MARK(0);
     const int bid = blockIdx.x;
     const int split = bid % a.P;
     const int yg = (bid / a.P) % a.n_yg;
@@ -474,6 +483,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
             }
             qf[s] = v;
         }
+        LMX_DECODE_MARK(1);
 
         // Online-softmax state.  Each 16-lane group g4 runs its own stream over
         // keys 4g4..4g4+3 of every tile: lane (c16 < GB, g4) holds the running
@@ -559,6 +569,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) asm volatile("" : "+v"(o[h][d]));
             asm volatile("" : "+v"(m_run), "+v"(l_run));
+            if (t == tile_of(0)) LMX_DECODE_MARK(2);
         };
 
         if constexpr (PIPE) {
@@ -599,6 +610,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
             }
         }
 
+        LMX_DECODE_MARK(3);
         // Combine the wave's four group streams: M = max of the group maxima;
         // group g is weighted by exp2(m_g - M), in l and in o.
         float M = fmaxf(m_run, shfl_xor(m_run, 16));
@@ -696,6 +708,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
         }
     }
     if constexpr (WPH > 1) combine_waves();
+    LMX_DECODE_MARK(4);
 }
 
 struct DecodePlan {

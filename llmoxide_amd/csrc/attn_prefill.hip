@@ -1225,14 +1225,20 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
         }
         return cache + (size_t)s0 * a.kv_dim + kvh * HD;
     };
+    // Interior tiles by buffer loads from the tile's first row (one 32-bit
+    // offset a thread; the per-load strides in the scalar offset), as in
+    // attn_prefill_kernel.
+    static_assert(256 % KCH == 0 && 256 % (BN / 4) == 0, "uniform load strides");
+    const int kvb = a.kv_dim * 2;  // bytes per row
+    const int k_voff = (ctid / KCH) * kvb + (ctid % KCH) * 16;
+    const int v_voff = 4 * (ctid % (BN / 4)) * kvb + (ctid / (BN / 4)) * 16;
     auto fetch_k = [&](int kt) {
         if (const f16* kb = fast_base(a.k, a.k_cur, kt)) {
+            const __amdgpu_buffer_rsrc_t src = make_rsrc(kb);
 #pragma unroll
-            for (int i = 0; i < KPT; ++i) {
-                const int c = ctid + 256 * i;
-                const int key = c / KCH, col = c - key * KCH;
-                rk[i] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * a.kv_dim + col * 8);
-            }
+            for (int i = 0; i < KPT; ++i)
+                rk[i] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(src, k_voff, i * (256 / KCH) * kvb, 0));
             return;
         }
 #pragma unroll
@@ -1248,15 +1254,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_pp_kernel(PrefillArgs a) 
     };
     auto fetch_v = [&](int kt) {
         if (const f16* vb = fast_base(a.v, a.v_cur, kt)) {
+            const __amdgpu_buffer_rsrc_t src = make_rsrc(vb);
 #pragma unroll
-            for (int i = 0; i < VPT; ++i) {
-                const int pr = ctid + 256 * i;
-                const int kg = pr % (BN / 4), dc = pr / (BN / 4);
-                if (pr < KCH * (BN / 4))
+            for (int i = 0; i < VPT; ++i)
+                if (ctid + 256 * i < KCH * (BN / 4))
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        rv[i][u] = *reinterpret_cast<const f16x8*>(vb + (size_t)(4 * kg + u) * a.kv_dim + dc * 8);
-            }
+                        rv[i][u] = __builtin_bit_cast(
+                            f16x8, __builtin_amdgcn_raw_buffer_load_b128(src, v_voff + i * (256 / (BN / 4)) * 16,
+                                                                          u * kvb, 0));
             return;
         }
 #pragma unroll
