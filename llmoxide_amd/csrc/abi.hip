@@ -175,7 +175,7 @@ static lmx_status scratch_of_stream_device(hipStream_t stream, void** out) {
 }
 
 // ---- tuning overrides (see Tuning in common.hpp)
-static std::atomic<int> g_tune_kernel{-1}, g_tune_gp{0}, g_tune_kh{-1}, g_tune_krows{-1};
+static std::atomic<int> g_tune_kernel{-1}, g_tune_gp{0}, g_tune_kh{-1}, g_tune_krows{-1}, g_tune_mh{-1};
 static std::once_flag g_tune_once;
 
 static void read_tuning_env() {
@@ -192,11 +192,13 @@ static void read_tuning_env() {
     const char* kh = std::getenv("LMX_PREFILL_KH");
     g_tune_kh.store(kh && kh[0] == '0' ? 0 : -1);
     g_tune_krows.store(choice("LMX_DECODE_KROWS", "1", 1, "0", 0));
+    const char* mh = std::getenv("LMX_DECODE_MH");
+    g_tune_mh.store(mh && mh[0] == '0' ? 0 : -1);
 }
 
 Tuning tuning() {
     std::call_once(g_tune_once, read_tuning_env);
-    return Tuning{g_tune_kernel.load(), g_tune_gp.load(), g_tune_kh.load(), g_tune_krows.load()};
+    return Tuning{g_tune_kernel.load(), g_tune_gp.load(), g_tune_kh.load(), g_tune_krows.load(), g_tune_mh.load()};
 }
 
 }  // namespace lmx

@@ -90,19 +90,28 @@ static bool pick_krows(int hd, int mode, const DecodePlan& pl) {
     return mode == kModeBatched || pl.n_main > kCusPerGpu || tiles_per_wave <= 4;
 }
 
+// Head_dim 512 with 16 query heads a kv head (Gemma 4's global layers) takes
+// attn_decode_mh_kernel: a workgroup serves the 16 heads and every tile of its
+// split, each wave a quarter of the output dims.  Splits of at least
+// kMhMinTiles tiles (32 KB of K and V each) amortise its Q load.
+// LMX_DECODE_MH=0 keeps attn_decode_kernel (tuning overrides, for tests).
+constexpr long kMhMinTiles = 4;
+static bool use_mh(int G, int hd) { return hd == 512 && G % kMhHeads == 0 && tuning().decode_mh != 0; }
+
 // n_q query rows (tokens or sequences), longest visible range max_vis.
 static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis, int mode) {
     DecodePlan pl{};
     const int G = H / Hkv;
-    pl.gb = pick_gb(G, hd);
+    pl.mh = use_mh(G, hd);
+    pl.gb = pl.mh ? kMhHeads : pick_gb(G, hd);
     pl.n_hblk = G / pl.gb;
-    pl.hw = pick_hw(Hkv);
+    pl.hw = pl.mh ? 1 : pick_hw(Hkv);
     pl.n_yg = (Hkv / pl.hw) * pl.n_hblk;
     const long units = (long)n_q * pl.n_yg;
     const long n_tiles = (max_vis + kTile - 1) / kTile;
-    const long wph = kWaves / pl.hw;
+    const long wph = pl.mh ? 1 : kWaves / pl.hw;  // the mh kernel's waves all take every tile
     long P = (target_wgs(n_q) + units - 1) / units;
-    const long cap = n_tiles / (wph * min_tiles_per_wave(hd));
+    const long cap = n_tiles / (wph * (pl.mh ? kMhMinTiles : min_tiles_per_wave(hd)));
     if (P > cap) P = cap;
     if (P > kMaxP) P = kMaxP;
     if (P < 1) P = 1;
@@ -129,7 +138,7 @@ static DecodePlan plan_decode(int n_q, int H, int Hkv, int hd, int max_vis, int 
         pl.ml_bytes = round_up((size_t)n_q * H * P * 2 * 4, 256);
         pl.o_bytes = round_up((size_t)n_q * H * P * hd * 4, 256);
     }
-    pl.krows = pick_krows(hd, mode, pl);
+    pl.krows = !pl.mh && pick_krows(hd, mode, pl);
     if (pl.P_ws > 1)
         pl.ws_bytes = round_up((size_t)n_q * H * pl.P_ws * 2 * 4, 256) +
                       round_up((size_t)n_q * H * pl.P_ws * hd * 4, 256);

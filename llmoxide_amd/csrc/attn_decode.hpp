@@ -66,7 +66,8 @@ enum DecodeMode { kModeLinear = 0, kModeGeneral = 1, kModeBatched = 2 };
 // Timeline hook: a measurement build defines LMX_DECODE_MARK(i) before
 // including this header (llmoxide_amd/timeline/decode_timeline.hip stores each
 // wave's s_memrealtime at phase i: 0 entry, 1 query converted, 2 first tile
-// done, 3 last tile done, 4 partials stored).  The library leaves it empty.
+// done, 3 last tile done, 4 partials stored), in attn_decode_kernel and
+// attn_decode_mh_kernel.  The library leaves it empty.
 #ifndef LMX_DECODE_MARK
 #define LMX_DECODE_MARK(i) ((void)0)
 #endif
@@ -711,12 +712,278 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(DecodeArgs a) 
     LMX_DECODE_MARK(4);
 }
 
+// ---- Many query heads on one kv head at head_dim 512 (Gemma 4's global
+// layers: 16 query heads share each kv head) --------------------------------
+//
+// attn_decode_kernel does P.V on the VALU, one query head's dims per lane
+// set, and at head_dim 512 holds at most four heads a wave: the 16 heads of
+// a kv head then stream its rows four times and spend 268 M FMAs a 32k call
+// on the VALU.  Here a workgroup serves all 16 heads of a kv head and split
+// s of its tiles, and both products run on the matrix cores:
+//
+//   S^T [16 keys x 16 heads] = K Q^T on v_mfma_f32_16x16x32_f16: A = the K
+//     tile (lane (key c16, group g4) holds dims 32 s + 8 g4 .. + 7), B = Q^T
+//     (column c16 = head h0 + c16; an fp32 query's f16 residual is a second
+//     column block whose result adds in place).  Lane (g4, c16) then holds
+//     keys 4 g4 .. + 3 of head c16: the B operand layout of
+//   O^T [16 dims x 16 heads] += V^T P^T on v_mfma_f32_16x16x16_f16: A = V^T,
+//     4 keys of one dim a lane, read out of the wave's row-major V tile in
+//     LDS with ds_read_b64_tr_b16 (lane a + 4 j addresses key 4 g4 + j, dims
+//     16 db + 4 a .. + 3; lane c16 receives keys 4 g4 .. + 3 of dim
+//     16 db + c16).
+//
+// The four waves take the head's 512 output dims in quarters and every tile
+// of the split; each forms the same scores (the matrix pipe has room: 32 or
+// 16 MFMAs a 32 KB tile), so m and l agree across them and no wave merge is
+// needed.  A head's running max sits in the four lanes (g4 = 0..3) of its
+// column; each lane sums its own keys' p, combined at the end.  Partials
+// (p_u > 1) go to the same layout attn_merge_kernel<512> reads.
+constexpr int kMhHeads = 16;  // query heads a workgroup (one MFMA column block)
+#ifndef LMX_MH_DEPTH
+#define LMX_MH_DEPTH 2
+#endif
+constexpr int kMhDepth = LMX_MH_DEPTH;  // tiles in flight a wave
+
+template <typename QT, int MODE>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_mh_kernel(DecodeArgs a) {
+    constexpr int HD = 512, KS = HD / 32;  // score MFMA k-steps
+    constexpr int DW = HD / kWaves;        // output dims a wave owns
+    constexpr int NDB = DW / 16;           // its 16-dim output blocks
+    constexpr int VPAD = DW + 8;           // V_s row stride (halfs)
+    constexpr bool SPLIT_Q = sizeof(QT) == 4;
+    args_in_sgprs(a.q, a.out, a.gate, a.part_o, a.part_ml, a.q_stride, a.gate_stride, a.H, a.G, a.kv_dim, a.P,
+                  a.tps, a.n_hblk, a.n_yg, a.window, a.c);
+    if constexpr (MODE == kModeBatched)
+        args_in_sgprs(a.k_ptrs, a.v_ptrs, a.ctx_lens, a.max_ctx);
+    else
+        args_in_sgprs(a.k, a.v, a.k_cur, a.v_cur, a.base_pos, a.n_tokens, a.bidi, a.w_magic, a.w_shift);
+    LMX_DECODE_MARK(0);
+    const int bid = blockIdx.x;
+    const int split = bid % a.P;
+    const int yg = (bid / a.P) % a.n_yg;
+    const int qi = bid / (a.P * a.n_yg);
+    const int kvh = yg / a.n_hblk;
+    const int h0 = kvh * a.G + (yg - kvh * a.n_hblk) * kMhHeads;
+
+    int lo, hi;
+    unit_range<MODE>(a, qi, lo, hi);
+    const int n_tiles = (hi - lo + kTile) / kTile;
+    const int t_begin = split * a.tps;
+    if (t_begin >= n_tiles) return;  // uniform: this unit needs fewer splits
+    const int t_end = min(t_begin + a.tps, n_tiles);
+    const int p_u = (n_tiles + a.tps - 1) / a.tps;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g4 = lane >> 4, c16 = lane & 15;
+
+    const f16 *kc, *vc;
+    int cur_begin = INT_MAX;
+    if constexpr (MODE == kModeBatched) {
+        kc = a.k_ptrs[qi];
+        vc = a.v_ptrs[qi];
+    } else {
+        kc = a.k;
+        vc = a.v;
+        if (MODE == kModeGeneral && a.k_cur) cur_begin = a.base_pos;
+    }
+    auto row_ptr = [&](const f16* cache, const f16* cur, int p) -> const f16* {
+        if constexpr (MODE == kModeLinear) {
+            return cache + (size_t)p * a.kv_dim + kvh * HD;
+        } else {
+            int s = p;
+            if (a.window) {
+                const uint32_t qd = (uint32_t)(((uint64_t)(uint32_t)p * a.w_magic) >> a.w_shift);
+                s = p - (int)qd * a.window;
+            }
+            const f16* rc = cache + (size_t)s * a.kv_dim;
+            const f16* ru = cur + (size_t)(p - a.base_pos) * a.kv_dim;
+            return (p >= cur_begin ? ru : rc) + kvh * HD;
+        }
+    };
+
+    // Each wave holds and loads its quarter of the head's dims: Q^T k-steps
+    // (32 dims each) KQ w .. KQ w + KQ - 1, the K tile's same dims, and V's
+    // dims DW w .. + DW - 1.  The partial scores of the four quarters are
+    // summed through LDS; with 8 KB a tile a wave, MH_DEPTH tiles are in flight
+    // (the first form, every wave loading the whole K tile with one tile
+    // ahead, ran at 2.2 TB/s).
+    constexpr int KQ = KS / kWaves;  // k-steps a wave owns
+    struct MhTile {
+        f16x8 k[KQ];  // key c16 of the tile, dims 32 (KQ w + s) + 8 g4 .. + 7
+        f16x8 v[4];   // key 4 i + g4, dims DW w + 8 c16 .. + 7
+    };
+    // Rows past hi are clamped to hi (their scores are masked).
+    auto load_tile = [&](int t, MhTile& b) {
+        const int kt = lo + kTile * t;
+        const f16* krow = row_ptr(kc, a.k_cur, min(kt + c16, hi)) + DW * wave;
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) b.k[s] = ld_stream8<true>(krow + 32 * s + 8 * g4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            b.v[i] = ld_stream8<true>(row_ptr(vc, a.v_cur, min(kt + 4 * i + g4, hi)) + DW * wave + 8 * c16);
+    };
+
+    // Q^T columns: head h0 + c16, this wave's dims (f16, and an fp32 query's
+    // f16 residual).  The raw loads go out first, then the first tiles', and
+    // only then the conversion waits.
+    using QRaw = typename std::conditional<SPLIT_Q, f32x4, f16x8>::type;
+    QRaw qraw[KQ][SPLIT_Q ? 2 : 1];
+    {
+        const size_t qo = ((size_t)qi * a.H + h0 + c16) * a.q_stride + DW * wave + 8 * g4;
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) {
+            if constexpr (SPLIT_Q) {
+                const float* qp = reinterpret_cast<const float*>(a.q) + qo + 32 * s;
+                qraw[s][0] = *reinterpret_cast<const f32x4*>(qp);
+                qraw[s][SPLIT_Q ? 1 : 0] = *reinterpret_cast<const f32x4*>(qp + 4);
+            } else {
+                qraw[s][0] = *reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(a.q) + qo + 32 * s);
+            }
+        }
+    }
+    const int my_n = t_end - t_begin;  // every wave takes every tile of the split
+    MhTile bufs[kMhDepth];
+#pragma unroll
+    for (int k = 0; k < kMhDepth; ++k) load_tile(t_begin + min(k, my_n - 1), bufs[k]);
+    __builtin_amdgcn_sched_barrier(0);
+    f16x8 qh[KQ], ql[SPLIT_Q ? KQ : 1];
+#pragma unroll
+    for (int s = 0; s < KQ; ++s) {
+        if constexpr (SPLIT_Q) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = qraw[s][j / 4][j % 4];
+                const f16 h = (f16)x;
+                qh[s][j] = h;
+                ql[s][j] = (f16)(x - (float)h);
+            }
+        } else {
+            qh[s] = qraw[s][0];
+        }
+    }
+    LMX_DECODE_MARK(1);
+
+    __shared__ __attribute__((aligned(16))) f16 V_s[kWaves][kTile][VPAD];
+    // Partial scores, two sets (tile parity): [set][wave][hi / lo block][lane]
+    __shared__ __attribute__((aligned(16))) f32x4 S_s[2][kWaves][2][64];
+    float m_run = -1e30f, l_run = 0.f;  // head c16: running max (log2 units); this lane's keys' sum
+    f32x4 o[NDB];                       // O^T block db: dims DW wave + 16 db + 4 g4 + i, head c16
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int t, const MhTile& b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<f16x8*>(&V_s[wave][4 * i + g4][8 * c16]) = b.v[i];
+        f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) {
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], qh[s], sh, 0, 0, 0);
+            if constexpr (SPLIT_Q) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[s], ql[s], sl, 0, 0, 0);
+        }
+        const int set = t & 1;
+        S_s[set][wave][0][lane] = sh;
+        if constexpr (SPLIT_Q) S_s[set][wave][1][lane] = sl;
+        // The set written here was last read two tiles ago, before the
+        // previous barrier; this barrier publishes it.
+        __syncthreads();
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};  // the same order in every wave: the same sums
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            sc += S_s[set][w][0][lane];
+            if constexpr (SPLIT_Q) sc += S_s[set][w][1][lane];
+        }
+        const int kt = lo + kTile * t;
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = kt + 4 * g4 + i <= hi ? sc[i] * a.c : -INFINITY;
+        float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        tm = fmaxf(tm, shfl_xor(tm, 16));
+        tm = fmaxf(tm, shfl_xor(tm, 32));
+        const float mn = fmaxf(m_run, tm);
+        const float corr = fast_exp2(m_run - mn);
+        m_run = mn;
+        f16x4 pf;
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pf[i] = (f16)fast_exp2(x[i] - mn);
+            ps += (float)pf[i];
+        }
+        l_run = l_run * corr + ps;
+        typedef __fp16 tr_h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+        typedef __attribute__((address_space(3))) tr_h4 lds_h4;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const f16x4 va = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (lds_h4*)&V_s[wave][4 * g4 + (c16 >> 2)][16 * db + 4 * (c16 & 3)]));
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pf, o[db] * corr, 0, 0, 0);
+        }
+        wave_lds_sync();  // the V reads are done before the next tile's writes
+        if (t == t_begin) LMX_DECODE_MARK(2);
+    };
+
+    // kMhDepth tiles in flight: a buffer is refilled with the tile kMhDepth
+    // ahead right after it is computed.  Rounds of kMhDepth while 2 kMhDepth
+    // - 1 tiles remain, then the last ones on uniform paths that load nothing
+    // past the split (every wave has the same count, so the barriers match).
+    int j = 0;
+    for (; j + 2 * kMhDepth - 1 < my_n; j += kMhDepth) {
+#pragma unroll
+        for (int k = 0; k < kMhDepth; ++k) {
+            compute(t_begin + j + k, bufs[k]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_tile(t_begin + j + kMhDepth + k, bufs[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const int rest = my_n - j;
+#pragma unroll
+    for (int k = 0; k < kMhDepth; ++k) {
+        if (k < rest) {
+            compute(t_begin + j + k, bufs[k]);
+            if (kMhDepth + k < rest) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_tile(t_begin + j + kMhDepth + k, bufs[k]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k + 1 < kMhDepth; ++k)
+        if (kMhDepth + k < rest) compute(t_begin + j + kMhDepth + k, bufs[k]);
+
+    LMX_DECODE_MARK(3);
+    // The head's sum over its four lanes; every wave holds the same m and L.
+    float L = l_run + shfl_xor(l_run, 16);
+    L += shfl_xor(L, 32);
+    const size_t row = (size_t)qi * a.H + h0 + c16;
+    if (p_u == 1) {
+        const float inv = 1.f / L;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const int d = DW * wave + 16 * db + 4 * g4;
+            f32x4 y = o[db] * inv;
+            if (a.gate) y = gate_sigmoid4(y, a.gate + row * a.gate_stride + d);
+            *reinterpret_cast<f32x4*>(a.out + row * HD + d) = y;
+        }
+    } else {
+        const size_t pidx = row * a.P + split;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+            *reinterpret_cast<f32x4*>(a.part_o + pidx * HD + DW * wave + 16 * db + 4 * g4) = o[db];
+        if (wave == 0 && g4 == 0) *reinterpret_cast<f32x2*>(a.part_ml + pidx * 2) = f32x2{m_run, L};
+    }
+    LMX_DECODE_MARK(4);
+}
+
 struct DecodePlan {
     int P, tps, n_hblk, gb, hw;
     int P_ws;          // splits the workspace is sized for (>= P)
     int n_main, n_yg;
     int n_merge, m_parts;
     bool krows;                // head_dim 128 / 256: K row-major through LDS (attn_decode_kernel's KR)
+    bool mh;                   // head_dim 512, 16 query heads a kv head: attn_decode_mh_kernel
     size_t ml_bytes, o_bytes;  // what this launch uses
     size_t ws_bytes;           // what the workspace query reports for this shape
     size_t total() const { return ml_bytes + o_bytes; }
@@ -772,7 +1039,11 @@ inline lmx_status launch_merge(const DecodeArgs& a, int hd, dim3 grid, hipStream
 // Enqueue the split kernel and, with more than one split, the merge kernel.
 template <typename QT, int MODE>
 lmx_status launch_mode(const DecodeArgs& a, const DecodePlan& pl, int hd, hipStream_t st) {
-    lmx_status s = launch_decode<QT, MODE>(a, hd, pl.gb, pl.hw, pl.krows, dim3((unsigned)pl.n_main), st);
+    lmx_status s = LMX_OK;
+    if (pl.mh)
+        hipLaunchKernelGGL((attn_decode_mh_kernel<QT, MODE>), dim3((unsigned)pl.n_main), dim3(kDecThreads), 0, st, a);
+    else
+        s = launch_decode<QT, MODE>(a, hd, pl.gb, pl.hw, pl.krows, dim3((unsigned)pl.n_main), st);
     if (s != LMX_OK || pl.P == 1) return s;
     return launch_merge<MODE>(a, hd, dim3((unsigned)pl.n_merge), st);
 }

@@ -1,23 +1,27 @@
 // Per-wave timeline of the decode split kernel at the C2 headline shape
-// (B = 1, 32768 keys, H 32 / Hkv 8 / head_dim 128, f16 K/V, fp32 query),
-// for measurement only: it is not part of libllmoxide_amd.so.
+// (B = 1, 32768 keys, H 32 / Hkv 8 / head_dim 128, f16 K/V, fp32 query), or
+// with the argument `gemma4` at Gemma 4's global-layer shape (H 16 / Hkv 1 /
+// head_dim 512, attn_decode_mh_kernel), for measurement only: it is not part
+// of libllmoxide_amd.so.
 //
 // It compiles the library's own kernel with LMX_DECODE_MARK defined, so that
 // lane 0 of every wave stores s_memrealtime (100 MHz) at the kernel's phase
 // marks, plus the wave's shader-clock cycles and its HW_ID / XCC_ID, then
 // prints the phase distribution over the 1024 waves of one call and the
-// per-XCD start / end.  The split plan is the library's for this shape
-// (2 units x 128 splits = 256 workgroups, 16 tiles a wave).
+// per-XCD start / end.  The split plans are the library's for these shapes
+// (headline: 2 units x 128 splits = 256 workgroups, 16 tiles a wave; gemma4:
+// 256 splits of 8 tiles, every wave taking every tile).
 //
 // Build and run (repository root):
 //   hipcc -O3 -std=c++17 --offload-arch=gfx950 -Xclang -target-feature \
 //     -Xclang -packed-fp32-ops -ffp-contract=fast -I include -I llmoxide_amd/csrc \
 //     llmoxide_amd/timeline/decode_timeline.hip -o /tmp/decode_timeline
-//   /tmp/decode_timeline
+//   /tmp/decode_timeline            (or: /tmp/decode_timeline gemma4)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdio>
+#include <string>
 #include <vector>
 
 __device__ unsigned long long g_tl[1024][8];
@@ -48,9 +52,13 @@ __device__ unsigned long long g_tl[1024][8];
         }                                                                                       \
     } while (0)
 
-int main() {
-    constexpr int H = 32, Hkv = 8, HD = 128, CTX = 32768, NL = 4;
-    constexpr int P = 128, TPS = 16, N_YG = 2, N_MAIN = 256;  // the library's plan for this shape
+int main(int argc, char** argv) {
+    const bool g4 = argc > 1 && std::string(argv[1]) == "gemma4";
+    const int H = g4 ? 16 : 32, Hkv = g4 ? 1 : 8, HD = g4 ? 512 : 128;
+    constexpr int CTX = 32768, NL = 4;
+    // the library's plans for these shapes
+    const int P = g4 ? 256 : 128, N_YG = g4 ? 1 : 2, N_MAIN = 256;
+    const int TPS = CTX / lmx::kTile / P;
     std::vector<float> hq(H * HD);
     unsigned s = 1;
     auto rnd = [&]() {
@@ -88,18 +96,30 @@ int main() {
     a.n_tokens = 1;
     a.P = P;
     a.tps = TPS;
-    a.n_hblk = 1;
+    a.n_hblk = 1;  // both shapes: one head block a kv head
     a.n_q = 1;
     a.n_main = N_MAIN;
     a.n_yg = N_YG;
-    a.m_parts = 16;
-    a.n_merge = (H * (HD / 4) * 16 + lmx::kDecThreads - 1) / lmx::kDecThreads;
-    a.c = 0.08838834764f * 1.4426950408889634f;
+    a.m_parts = g4 ? 32 : 16;  // lanes a merged column: P / 8 rounded up to a power of two
+    a.n_merge = (H * (HD / 4) * a.m_parts + lmx::kDecThreads - 1) / lmx::kDecThreads;
+    a.c = (g4 ? 1.0f : 0.08838834764f) * 1.4426950408889634f;
     auto split = [&](int l) {
         a.k = ks[l];
         a.v = vs[l];
-        hipLaunchKernelGGL((lmx::attn_decode_kernel<float, HD, 4, 4, lmx::kModeLinear, false>), dim3(N_MAIN),
-                           dim3(lmx::kDecThreads), 0, 0, a);
+        if (g4)
+            hipLaunchKernelGGL((lmx::attn_decode_mh_kernel<float, lmx::kModeLinear>), dim3(N_MAIN),
+                               dim3(lmx::kDecThreads), 0, 0, a);
+        else
+            hipLaunchKernelGGL((lmx::attn_decode_kernel<float, 128, 4, 4, lmx::kModeLinear, false>), dim3(N_MAIN),
+                               dim3(lmx::kDecThreads), 0, 0, a);
+    };
+    auto merge = [&]() {
+        if (g4)
+            hipLaunchKernelGGL((lmx::attn_merge_kernel<512, lmx::kModeLinear>), dim3(a.n_merge),
+                               dim3(lmx::kDecThreads), 0, 0, a);
+        else
+            hipLaunchKernelGGL((lmx::attn_merge_kernel<128, lmx::kModeLinear>), dim3(a.n_merge),
+                               dim3(lmx::kDecThreads), 0, 0, a);
     };
     for (int r = 0; r < 40; ++r) split(r % NL);
     CK(hipDeviceSynchronize());
@@ -110,8 +130,7 @@ int main() {
     CK(hipEventRecord(e0));
     for (int r = 0; r < REP; ++r) {
         split(r % NL);
-        hipLaunchKernelGGL((lmx::attn_merge_kernel<HD, lmx::kModeLinear>), dim3(a.n_merge), dim3(lmx::kDecThreads), 0,
-                           0, a);
+        merge();
     }
     CK(hipEventRecord(e1));
     CK(hipDeviceSynchronize());

@@ -211,3 +211,58 @@ def test_k_operand_paths(H, Hkv, hd, ctx, window, t, q_f16, tuning_env):
         outs.append(out.cpu().numpy())
         assert_close(outs[-1], ref, what=f"krows={krows}")
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("H,Hkv,ctx,window,t,q_f16,k_cur", [
+    (16, 1, 32768, 0, 1, False, False),   # Gemma 4 global layer at 32k, fp32 q (two column blocks)
+    (16, 1, 5000, 0, 1, True, False),     # f16 q (one column block)
+    (32, 2, 3000, 0, 2, False, False),    # two kv heads, two query rows
+    (64, 2, 2500, 0, 1, False, False),    # two 16-head blocks a kv head
+    (16, 1, 70, 0, 1, False, False),      # one split: the kernel writes the output itself
+    (16, 1, 2000, 512, 1, False, False),  # a ring (general addressing)
+    (16, 1, 900, 256, 3, True, True),     # a windowed batch whose rows come from k_cur
+])
+def test_many_heads_decode_hd512(H, Hkv, ctx, window, t, q_f16, k_cur, tuning_env):
+    """head_dim 512 with 16 query heads a kv head: attn_decode_mh_kernel (both
+    products on the matrix cores, all heads on one read of each row) against
+    the oracle, and against attn_decode_kernel (LMX_DECODE_MH=0) on the same
+    inputs."""
+    c = AttnCase(ctx + 31 * t + H + window, t=t, H=H, Hkv=Hkv, hd=512, n_pos=ctx, q_f16=q_f16, qk_norm=True)
+    base = ctx - t
+    outs = []
+    for mh in ("1", "0"):
+        tuning_env("LMX_DECODE_MH", mh)
+        say(f"hd 512 decode mh={mh} H={H} Hkv={Hkv} ctx={ctx} w={window} t={t} q_f16={q_f16} k_cur={k_cur}")
+        outs.append(run_case(c, base=base, window=window, ring=bool(window), k_cur=k_cur, scale=1.0))
+    say(f"  mh max_abs={outs[0][0]:.2e} / attn_decode_kernel {outs[1][0]:.2e}")
+
+
+def test_many_heads_decode_hd512_gate_and_batched():
+    """The output gate on both of the mh kernel's write paths (its own, with
+    one split, and the merge's), and ragged batched decode at head_dim 512
+    with 16 heads on one kv head."""
+    H, Hkv, hd = 16, 1, 512
+    for ctx in (60, 4000):
+        c = AttnCase(ctx + 5, t=1, H=H, Hkv=Hkv, hd=hd, n_pos=ctx, qk_norm=True)
+        gate = np.random.default_rng(ctx).standard_normal((1, H * hd)).astype(np.float32)
+        out = lmx.attention(dev(c.q), dev(c.k16, torch.float16), dev(c.v16, torch.float16), n_heads=H,
+                            n_kv_heads=Hkv, head_dim=hd, base_pos=ctx - 1, scale=1.0, gate=dev(gate))
+        torch.cuda.synchronize()
+        ref = c.reference(base_pos=ctx - 1, scale=1.0) / (1.0 + np.exp(-gate.astype(np.float64)))
+        assert_close(out.cpu().numpy(), ref, what=f"gated hd 512 ctx {ctx}")
+    lens = [33, 700, 4096, 1999]
+    ks, vs, qs, refs = [], [], [], []
+    for i, n in enumerate(lens):
+        c = AttnCase(900 + i, t=1, H=H, Hkv=Hkv, hd=hd, n_pos=n, qk_norm=True)
+        refs.append(c.reference(base_pos=n - 1, scale=1.0))
+        qs.append(c.q)
+        ks.append(dev(c.k16, torch.float16))
+        vs.append(dev(c.v16, torch.float16))
+    max_ctx = max(lens)
+    out = lmx.attention_decode_batched(dev(np.concatenate(qs)), lmx.BatchedCaches(ks, vs),
+                                       dev(np.array(lens, np.int32)), max_ctx=max_ctx, n_heads=H,
+                                       n_kv_heads=Hkv, head_dim=hd, n_slots=max_ctx, scale=1.0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, n in enumerate(lens):
+        assert_close(got[i:i + 1], refs[i], what=f"batched hd 512 seq {i} ctx {n}")

@@ -168,9 +168,9 @@ def test_full_size_sampled_rows(S, base):
 @pytest.mark.parametrize("t,base", [(300, 0), (2048, 0), (64, 6000), (333, 50)])
 def test_head_dim_512_prefill(t, base):
     """Gemma 4 global layers: head_dim 512, one kv head (ARCHITECTURE.md:25-28;
-    attn.wgsl:44-46 takes hd <= 512).  Two workgroups share each (head,
-    query tile), one per half of the output dims; a short chunk on a long
-    cache also takes key splits."""
+    attn.wgsl:44-46 takes hd <= 512).  Two waves share each 32-row block, one
+    per half of the head's dims, and sum their partial scores through LDS; a
+    short chunk on a long cache also takes key splits."""
     c = AttnCase(512 + t + base, t=t, H=16, Hkv=1, hd=512, n_pos=base + t, q_f16=True, qk_norm=True)
     check(c, base=base, scale=1.0 / np.sqrt(512))
 
@@ -178,6 +178,26 @@ def test_head_dim_512_prefill(t, base):
 def test_head_dim_512_sliding_window_with_k_cur():
     c = AttnCase(5120, t=700, H=8, Hkv=2, hd=512, n_pos=1700, q_f16=True)
     check(c, base=1000, window=512, ring=True, k_cur=True, scale=1.0 / np.sqrt(512))
+
+
+@pytest.mark.parametrize("gp", [1, 2])
+@pytest.mark.parametrize("mode", ["causal", "ring", "bidi"])
+def test_head_dim_512_wave_pairs_heads_per_workgroup(gp, mode, tuning_env):
+    """The head_dim-512 wave pairs with one or two query heads a workgroup
+    (two 32-row blocks of one head, or one block of each of two heads):
+    ragged t, rows before the batch, a ring read with k_cur rows, and a
+    bidirectional batch (every wave meets the partial-score barrier, also on
+    tiles outside its own rows' range)."""
+    tuning_env("LMX_PREFILL_GP", str(gp))
+    say(f"hd 512 wave pairs gp={gp} {mode}")
+    c = AttnCase(700 + 10 * gp + len(mode), t=197, H=8, Hkv=2, hd=512, n_pos=197 + 300, q_f16=True,
+                 qk_norm=True)
+    if mode == "ring":
+        check(c, base=300, window=256, ring=True, k_cur=True, scale=1.0)
+    elif mode == "bidi":
+        check(c, base=0, bidi=True, scale=1.0 / np.sqrt(512))
+    else:
+        check(c, base=300, scale=1.0 / np.sqrt(512))
 
 
 @pytest.mark.parametrize("kh", ["1", "0"])
