@@ -83,8 +83,6 @@ __device__ __forceinline__ int vis_hi(int pos, int w, int bidi, int end) {
     return w ? min(end, pos + w - 1) : end;
 }
 
-// Bijective block remap so that consecutive logical ids share an XCD (blocks
-// are dispatched round-robin over 8 XCDs).
 // S^T - mb = K Q^T - mb for KB 32-key blocks of a K tile in LDS (rows of
 // KPAD halfs), Q^T in registers as the B operand.  The K operand reads run
 // QK_DEPTH ahead of the MFMAs (the compiler's own schedule kept one or two
@@ -194,12 +192,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
     void* q = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
     return __builtin_amdgcn_make_buffer_rsrc(q, 0, 0x7fffffff, 0x00020000);
-}
-
-__device__ __forceinline__ int xcd_remap(int bid, int n) {
-    const int q = n / 8, r = n % 8;
-    const int xcd = bid % 8, local = bid / 8;
-    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
 // LIN: every key row p lives at cache row p (no k_cur rows, no ring wrap),

@@ -180,6 +180,15 @@ __device__ __forceinline__ int ring_slot(int p, int w, uint32_t magic, int shift
     return p - (int)q * w;
 }
 
+// Bijective workgroup remap so that consecutive logical ids share an XCD
+// (workgroups are dispatched round-robin over the 8 XCDs): XCD x runs a
+// contiguous range of about n / 8 logical ids.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+    const int q = n / 8, r = n % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
 }  // namespace lmx
 
 // Host-side helpers shared by the entry points.

@@ -6,15 +6,19 @@
 // conv_commit, l2norm_qk; deltanet.wgsl:54-173): the conv output makes a
 // round trip through HBM before the norm, and the window update goes through
 // a scratch copy so that no thread reads a row another one is overwriting.
-// Here one workgroup owns a 128-channel block (one q/k head at s_dim 128)
-// for a chunk of 64 tokens: each wave takes 16 consecutive tokens, a lane
-// holds two channels (lane and lane + 64), the K-1 rows before the wave's
-// tokens (from the batch, or before it from the window) and its own rows are
-// loaded once into registers, the taps slide over them in the reference's
-// order, and the head's L2 norm is a wave reduction, so each output row is
-// written once.  Only the first chunk's workgroup of a block
-// reads the old window, so it alone writes the new one, after its own reads:
-// no workgroup ever reads a window row another one writes.
+// Here one launch does it all.  A wave owns a block of channels for a run of
+// consecutive tokens: the K-1 rows before its tokens (from the batch, or
+// before it from the window) and its own rows are loaded once into
+// registers, the taps slide over them in the reference's order, and the
+// head's L2 norm is a wave reduction, so each output row is written once.
+// Two forms: with x, the window and the output 16-byte aligned, a lane holds
+// four channels (one 16-byte access a row) and a wave takes 256 channels x 8
+// tokens; otherwise a lane holds two (lane and lane + 64) and a wave takes
+// 128 channels x 16 tokens.  Workgroups are remapped so that each XCD runs a
+// contiguous range of tokens across all channels.  Only the first chunk's
+// workgroup of a block reads the old window, so it alone writes the new one,
+// after its own reads: no workgroup ever reads a window row another one
+// writes.
 //
 // Back.  rms_norm over each v-head then mul_silu (qwen35.rs:968-986): one
 // wave per (token, v-head) row, one pass.
@@ -24,7 +28,13 @@ namespace lmx {
 
 constexpr int kFrontTokens = 64;  // tokens per front workgroup (>= kernel - 1)
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+// x / (1 + e^-x) as x * rcp(1 + 2^(-x log2 e)): the hardware exp2 and
+// reciprocal (1 ulp each) in place of the libm-accurate expf and the IEEE
+// divide.  The rounding of -x log2 e moves e^-x by about |x| 2^-24 relative,
+// so while e^-x is finite (x > -88) the result is within about
+// (|x| + 2) 2^-24 of the exact SiLU, relative; below that it is 0 where the
+// exact value is under 1e-36.
+__device__ __forceinline__ float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 struct FrontArgs {
     const float* x;
@@ -35,9 +45,20 @@ struct FrontArgs {
     float eps;
 };
 
+// Workgroup (block, chunk) of an n_cb x n_tc grid launched 1-D: with the XCD
+// remap each XCD runs a contiguous run of token chunks across every channel
+// block (whole rows), rather than the same channel columns of every row.
+__device__ __forceinline__ void front_tile(int n_cb, int* cb, int* tc) {
+    const int n = (int)gridDim.x;
+    const int t = xcd_remap((int)blockIdx.x, n);
+    *cb = t % n_cb;
+    *tc = t / n_cb;
+}
+
 template <int K>
 __global__ __launch_bounds__(256) void delta_front_kernel(FrontArgs a) {
-    const int cb = blockIdx.x, tc = blockIdx.y;
+    int cb, tc;
+    front_tile(a.conv_dim / 128, &cb, &tc);
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c0 = cb * 128 + lane, c1 = c0 + 64;
@@ -128,6 +149,114 @@ __global__ __launch_bounds__(256) void delta_front_kernel(FrontArgs a) {
     }
 }
 
+// SiLU, then the per-head L2 norm on q/k channels, of one conv row held four
+// channels a lane (the head's s_dim / 4 lanes sum its squares; s_dim is 64
+// or 128).
+__device__ __forceinline__ f32x4 front_finish(f32x4 acc, bool qk, int lane, int s_dim, float eps) {
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = silu_f(acc[e]);
+    // ops.rs:197-203: x / max(||x||, eps) per head
+    float ss = row_sum16((y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]));
+    if (s_dim == 128) {  // two DPP rows a head: rows 0 + 1 and 2 + 3
+        const int b = __builtin_bit_cast(int, ss);
+        const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+        const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+        const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+        const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+        ss = lane < 32 ? r0 + r1 : r2 + r3;
+    }
+    if (qk) y *= 1.f / fmaxf(sqrtf(ss), eps);
+    return y;
+}
+
+// The 16-byte form (x, out and the window 16-byte aligned): a lane holds
+// four consecutive channels, so a wave covers a 256-channel block and each
+// row it touches is one 16-byte load or store a lane.  A workgroup's four
+// waves take 8 consecutive tokens each; as in the two-channel form, a wave
+// loads the K-1 rows before its first token and its own 8 rows once (the
+// rows it shares with its neighbour come from L2), then stores 8 rows.
+constexpr int kFront4Wave = 8;
+constexpr int kFront4Tokens = 4 * kFront4Wave;
+static_assert(kFront4Tokens >= 7, "only the first chunk may touch the old window");
+
+// One wave's rows.  INTERIOR (no window rows, all NT rows inside the batch,
+// all 256 channels live) is straight-line code with unconditional loads and
+// stores; the checks an edge wave needs cost the interior ones about a tenth
+// of the kernel's time when they sit in its one path.
+template <int K, bool INTERIOR>
+__device__ __forceinline__ void front4_rows(const FrontArgs& a, const f32x4 (&tp)[K], int c, bool live, bool qk,
+                                            int lane, int tok0) {
+    constexpr int NT = kFront4Wave;
+    const int nt = min(NT, a.n_tok - tok0);
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 r[NT + K - 1];
+#pragma unroll
+    for (int idx = 0; idx < NT + K - 1; ++idx) {
+        const int p = tok0 - (K - 1) + idx;  // position p of [window | x]
+        if (INTERIOR) {
+            r[idx] = *reinterpret_cast<const f32x4*>(a.x + (size_t)p * a.conv_dim + c);
+        } else {
+            const float* row = p >= 0 ? a.x + (size_t)p * a.conv_dim : a.state + (size_t)(p + K - 1) * a.conv_dim;
+            r[idx] = (p < a.n_tok && live) ? *reinterpret_cast<const f32x4*>(row + c) : z4;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        if (!INTERIOR && i >= nt) continue;  // uniform
+        // qwen35/cpu.rs:200-204: the current row's term first, then the
+        // window rows oldest first
+        f32x4 acc = r[i + K - 1] * tp[K - 1];
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) acc += r[i + j] * tp[j];
+        const f32x4 y = front_finish(acc, qk, lane, a.s_dim, a.eps);
+        if (INTERIOR || live) *reinterpret_cast<f32x4*>(a.out + (size_t)(tok0 + i) * a.conv_dim + c) = y;
+    }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void delta_front4_kernel(FrontArgs a) {
+    int cb, tc;
+    front_tile((a.conv_dim + 255) / 256, &cb, &tc);
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = cb * 256 + 4 * lane;  // this lane's channels c .. c + 3
+    const bool live = c < a.conv_dim;   // conv_dim % 128 == 0: all four or none
+    const bool qk = c < 2 * a.key_dim;  // whole heads on either side (s_dim | key_dim)
+    const int cl = live ? c : 0;        // taps of a dead lane: any in-bounds row
+    f32x4 tp[K];                        // tp[j][e] = taps[c + e][j]
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < K; ++j) tp[j][e] = a.taps[(size_t)(cl + e) * K + j];
+    const int tok0 = tc * kFront4Tokens + kFront4Wave * w;
+    // uniform per wave
+    if (tok0 >= K - 1 && tok0 + kFront4Wave <= a.n_tok && cb * 256 + 256 <= a.conv_dim)
+        front4_rows<K, true>(a, tp, c, live, qk, lane, tok0);
+    else if (tok0 < a.n_tok)
+        front4_rows<K, false>(a, tp, c, live, qk, lane, tok0);
+
+    // The window after the batch (as in delta_front_kernel): the first
+    // chunk's workgroup is the only reader of the old window for this block.
+    if (tc == 0) {
+        constexpr int PW = (K - 1 + 3) / 4;
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 nw[PW];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int rr = w + 4 * k, p = a.n_tok + rr - (K - 1);
+            const float* row = p >= 0 ? a.x + (size_t)p * a.conv_dim : a.state + (size_t)(p + K - 1) * a.conv_dim;
+            nw[k] = (rr < K - 1 && live) ? *reinterpret_cast<const f32x4*>(row + c) : z4;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int rr = w + 4 * k;
+            if (rr < K - 1 && live) *reinterpret_cast<f32x4*>(a.state + (size_t)rr * a.conv_dim + c) = nw[k];
+        }
+    }
+}
+
 // NJ = s_dim / 64: lane l holds channels l + 64 j of its row.
 template <int NJ>
 __global__ __launch_bounds__(256) void delta_back_kernel(float* __restrict__ o,
@@ -169,11 +298,19 @@ lmx_status deltanet_front(const lmx_delta_front_desc* d, const float* x, const f
     a.s_dim = (int)d->s_dim;
     a.kernel = (int)d->kernel;
     a.eps = d->eps;
-    const dim3 grid(d->conv_dim / 128, (d->n_tok + kFrontTokens - 1) / kFrontTokens);
+    // The 16-byte form where every buffer is 16-byte aligned (rows are then
+    // 16-byte multiples too: conv_dim % 128 == 0).
+    const bool v4 = ((uintptr_t)x | (uintptr_t)conv_state | (uintptr_t)conv_out) % 16 == 0;
+    const int n_cb = v4 ? (d->conv_dim + 255) / 256 : d->conv_dim / 128;
+    const int tpw = v4 ? kFront4Tokens : kFrontTokens;
+    const dim3 grid(n_cb * ((d->n_tok + tpw - 1) / tpw));
     (void)hipGetLastError();
     switch (d->kernel) {
-#define LMX_FRONT(KV) \
-    case KV: hipLaunchKernelGGL(delta_front_kernel<KV>, grid, dim3(256), 0, st, a); break;
+#define LMX_FRONT(KV)                                                                  \
+    case KV:                                                                           \
+        if (v4) hipLaunchKernelGGL(delta_front4_kernel<KV>, grid, dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL(delta_front_kernel<KV>, grid, dim3(256), 0, st, a);     \
+        break;
         LMX_FRONT(2) LMX_FRONT(3) LMX_FRONT(4) LMX_FRONT(5) LMX_FRONT(6) LMX_FRONT(7) LMX_FRONT(8)
 #undef LMX_FRONT
         default: return LMX_E_UNSUPPORTED;

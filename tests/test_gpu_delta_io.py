@@ -40,6 +40,51 @@ def test_front_matches_oracle(shape, t):
     np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)  # the window is copied, bit for bit
 
 
+@pytest.mark.parametrize("t", [67, 200])
+@pytest.mark.parametrize("shape", [dict(conv_dim=384, key_dim=128, s_dim=64, kernel=4),
+                                   dict(conv_dim=1280, key_dim=256, s_dim=128, kernel=3),
+                                   dict(conv_dim=1536, key_dim=256, s_dim=128, kernel=6),
+                                   dict(conv_dim=2048, key_dim=512, s_dim=64, kernel=8)],
+                         ids=["two_channel", "one_wave_of_four", "k6_two_waves", "k8"])
+def test_front_block_edges(shape, t):
+    """conv_dim % 256 == 128 takes the two-channel kernel; the others stream
+    with a last workgroup only partly inside conv_dim, q/k and v channels in
+    one wave, a full segment then a ragged one, and kernels up to 8 taps."""
+    say(f"delta front edges {shape} t={t}")
+    x, taps, state = front_inputs(shape, t, 11)
+    kw = dict(key_dim=shape["key_dim"], s_dim=shape["s_dim"])
+    ref, st_ref = oracle.delta_front(x, taps, state, **kw)
+    sd = dev(state)
+    out = lmx.delta_front(dev(x), dev(taps), sd, **kw)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out")
+    np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)
+
+
+def test_front_unaligned_input_takes_the_two_channel_form():
+    """x 4 bytes off a 16-byte boundary: the two-channel kernel runs. Both forms
+    meet the oracle; they sum the head norm in different orders, so their
+    outputs may differ in the last bit, and the windows are equal."""
+    say("delta front unaligned x")
+    t = 70
+    x, taps, state = front_inputs(C5, t, 12)
+    kw = dict(key_dim=C5["key_dim"], s_dim=C5["s_dim"])
+    ref, st_ref = oracle.delta_front(x, taps, state, **kw)
+    flat = torch.zeros(t * C5["conv_dim"] + 4, dtype=torch.float32, device="cuda")
+    xu = flat[1:1 + t * C5["conv_dim"]].view(t, C5["conv_dim"])
+    xu.copy_(dev(x))
+    assert xu.data_ptr() % 16 == 4
+    sd_u, sd_a = dev(state), dev(state)
+    out_u = lmx.delta_front(xu, dev(taps), sd_u, **kw)
+    out_a = lmx.delta_front(dev(x), dev(taps), sd_a, **kw)
+    torch.cuda.synchronize()
+    assert_close(out_u.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out (two-channel)")
+    assert_close(out_a.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out (16-byte)")
+    np.testing.assert_allclose(out_u.cpu().numpy(), out_a.cpu().numpy(), rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(sd_u.cpu().numpy(), st_ref)
+    np.testing.assert_array_equal(sd_a.cpu().numpy(), st_ref)
+
+
 def test_front_chained_calls_carry_the_window():
     say("delta front chained")
     x, taps, state = front_inputs(C5, 70, 4)
