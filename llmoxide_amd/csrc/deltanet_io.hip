@@ -20,8 +20,9 @@
 // after its own reads: no workgroup ever reads a window row another one
 // writes.
 //
-// Back.  rms_norm over each v-head then mul_silu (qwen35.rs:968-986): one
-// wave per (token, v-head) row, one pass.
+// Back.  rms_norm over each v-head then mul_silu (qwen35.rs:968-986), one
+// pass: with o, z and the weight 16-byte aligned a lane holds four channels
+// and a wave several (token, v-head) rows; otherwise one wave per row.
 #include "common.hpp"
 
 namespace lmx {
@@ -285,6 +286,68 @@ __global__ __launch_bounds__(256) void delta_back_kernel(float* __restrict__ o,
     }
 }
 
+// The 16-byte form of the back (o, z and the weight 16-byte aligned): a lane
+// holds four consecutive channels of a row, so a row is SD / 4 lanes and a
+// wave covers 64 / (SD / 4) rows at a step; it takes kBack4Steps steps, all
+// loaded before the first store.  The sum of squares is a DPP-row sum (SD
+// 64), two rows (128) or the whole wave (256).  Workgroups are XCD-remapped
+// so each XCD streams a contiguous range of rows; interior waves run without
+// the row checks.
+constexpr int kBack4Steps = 4;
+
+template <int SD, bool INTERIOR>
+__device__ __forceinline__ void back4_rows(float* __restrict__ o, const float* __restrict__ z, f32x4 wv,
+                                           int n_rows, float eps, int row0, int lane) {
+    constexpr int L = SD / 4, RPS = 64 / L, R = kBack4Steps;
+    const int sub = lane / L, c = 4 * (lane % L);
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 x[R], g[R];
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+        const int row = row0 + s * RPS + sub;
+        const bool in = INTERIOR || row < n_rows;
+        x[s] = in ? *reinterpret_cast<const f32x4*>(o + (size_t)row * SD + c) : z4;
+        g[s] = in ? *reinterpret_cast<const f32x4*>(z + (size_t)row * SD + c) : z4;
+    }
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+        float ss = (x[s][0] * x[s][0] + x[s][1] * x[s][1]) + (x[s][2] * x[s][2] + x[s][3] * x[s][3]);
+        if (L == 16) {
+            ss = row_sum16(ss);
+        } else if (L == 32) {  // two DPP rows a row of o: rows 0 + 1 and 2 + 3
+            const int b = __builtin_bit_cast(int, row_sum16(ss));
+            const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+            const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+            const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+            const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+            ss = lane < 32 ? r0 + r1 : r2 + r3;
+        } else {
+            ss = wave_sum64(ss);
+        }
+        // ops.rs:40-47, then the weight (ops.rs:53-59), then silu(z)
+        const float sc = 1.f / sqrtf(ss / (float)SD + eps);
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = x[s][e] * sc * wv[e] * silu_f(g[s][e]);
+        const int row = row0 + s * RPS + sub;
+        if (INTERIOR || row < n_rows) *reinterpret_cast<f32x4*>(o + (size_t)row * SD + c) = y;
+    }
+}
+
+template <int SD>
+__global__ __launch_bounds__(256) void delta_back4_kernel(float* __restrict__ o, const float* __restrict__ z,
+                                                          const float* __restrict__ wgt, int n_rows, float eps) {
+    constexpr int RPW = 64 / (SD / 4) * kBack4Steps;  // rows a wave
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = (t * 4 + w) * RPW;
+    if (row0 >= n_rows) return;  // wave-uniform; no barriers here
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(wgt + 4 * (lane % (SD / 4)));
+    if (row0 + RPW <= n_rows) back4_rows<SD, true>(o, z, wv, n_rows, eps, row0, lane);
+    else back4_rows<SD, false>(o, z, wv, n_rows, eps, row0, lane);
+}
+
 lmx_status deltanet_front(const lmx_delta_front_desc* d, const float* x, const float* taps,
                           float* conv_state, float* conv_out, hipStream_t st) {
     FrontArgs a{};
@@ -322,13 +385,25 @@ lmx_status deltanet_front(const lmx_delta_front_desc* d, const float* x, const f
 lmx_status deltanet_back(const lmx_delta_back_desc* d, float* o, const float* z, const float* w,
                          hipStream_t st) {
     const int n_rows = (int)(d->n_tok * d->n_vh);
-    const dim3 grid((n_rows + 3) / 4);
+    const bool v4 = ((uintptr_t)o | (uintptr_t)z | (uintptr_t)w) % 16 == 0;
     (void)hipGetLastError();
-    switch (d->s_dim) {
-        case 64: hipLaunchKernelGGL(delta_back_kernel<1>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
-        case 128: hipLaunchKernelGGL(delta_back_kernel<2>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
-        case 256: hipLaunchKernelGGL(delta_back_kernel<4>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
-        default: return LMX_E_UNSUPPORTED;
+    if (v4) {
+        const int rpg = 4 * (64 / (d->s_dim / 4)) * kBack4Steps;  // rows a workgroup
+        const dim3 grid((n_rows + rpg - 1) / rpg);
+        switch (d->s_dim) {
+            case 64: hipLaunchKernelGGL(delta_back4_kernel<64>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            case 128: hipLaunchKernelGGL(delta_back4_kernel<128>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            case 256: hipLaunchKernelGGL(delta_back4_kernel<256>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            default: return LMX_E_UNSUPPORTED;
+        }
+    } else {
+        const dim3 grid((n_rows + 3) / 4);
+        switch (d->s_dim) {
+            case 64: hipLaunchKernelGGL(delta_back_kernel<1>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            case 128: hipLaunchKernelGGL(delta_back_kernel<2>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            case 256: hipLaunchKernelGGL(delta_back_kernel<4>, grid, dim3(256), 0, st, o, z, w, n_rows, d->eps); break;
+            default: return LMX_E_UNSUPPORTED;
+        }
     }
     LMX_CHECK_LAUNCH();
     return LMX_OK;

@@ -97,10 +97,12 @@ def test_front_chained_calls_carry_the_window():
     np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)
 
 
+@pytest.mark.parametrize("n_vh,t", [(32, 37), (3, 37), (1, 1)], ids=["c5_heads", "ragged", "one_row"])
 @pytest.mark.parametrize("s_dim", [64, 128, 256])
-def test_back_matches_oracle(s_dim):
-    say(f"delta back s_dim={s_dim}")
-    n_vh, t = 32, 37
+def test_back_matches_oracle(s_dim, n_vh, t):
+    """16-byte form: whole workgroups, a ragged last wave (111 rows) and a
+    single row, at each head size."""
+    say(f"delta back s_dim={s_dim} n_vh={n_vh} t={t}")
     o = oracle.normal(s_dim + 1, (t, n_vh * s_dim))
     z = oracle.normal(s_dim + 2, (t, n_vh * s_dim))
     w = (1.0 + 0.2 * oracle.normal(s_dim + 3, (s_dim,))).astype(np.float32)
@@ -109,6 +111,25 @@ def test_back_matches_oracle(s_dim):
     lmx.delta_back(od, dev(z), dev(w), n_vh=n_vh, s_dim=s_dim)
     torch.cuda.synchronize()
     assert_close(od.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="o")
+
+
+def test_back_unaligned_gate_takes_the_row_form():
+    """z 4 bytes off a 16-byte boundary: the one-wave-a-row kernel runs and
+    meets the oracle."""
+    say("delta back unaligned z")
+    n_vh, t, s_dim = 32, 21, 128
+    o = oracle.normal(201, (t, n_vh * s_dim))
+    z = oracle.normal(202, (t, n_vh * s_dim))
+    w = (1.0 + 0.2 * oracle.normal(203, (s_dim,))).astype(np.float32)
+    ref = oracle.delta_back(o, z, w, n_vh=n_vh, s_dim=s_dim)
+    flat = torch.zeros(z.size + 4, dtype=torch.float32, device="cuda")
+    zu = flat[1:1 + z.size].view(z.shape)
+    zu.copy_(dev(z))
+    assert zu.data_ptr() % 16 == 4
+    od = dev(o)
+    lmx.delta_back(od, zu, dev(w), n_vh=n_vh, s_dim=s_dim)
+    torch.cuda.synchronize()
+    assert_close(od.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="o (row form)")
 
 
 def test_delta_layer_front_scan_back_matches_oracle():
