@@ -109,9 +109,13 @@ __global__ void zero_words(uint32_t* p, size_t n) {
 }
 
 // The same for 16-byte aligned buffers of whole 16-byte words (a KV slab).
+// Workgroups run round-robin over the 8 XCDs, so XCD x's workgroups
+// (b % 8 == x) take the x-th eighth of the buffer between them, rather than
+// the x-th 4 KB of every 32 KB; the grid is a multiple of 8.
 __global__ void zero_quads(uint4* p, size_t n) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x)
+    const unsigned per = gridDim.x / 8, xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    const size_t part = (n + 7) / 8, lo = xcd * part, hi = lo + part < n ? lo + part : n;
+    for (size_t i = lo + (size_t)local * blockDim.x + threadIdx.x; i < hi; i += (size_t)per * blockDim.x)
         p[i] = uint4{0u, 0u, 0u, 0u};
 }
 
@@ -240,6 +244,7 @@ lmx_status lmx_workspace_init(void* ws, size_t ws_bytes, lmx_stream stream) {
     const size_t n = ws_bytes / (quads ? 16 : 4);
     size_t blocks = (n + 255) / 256;
     if (blocks > 8192) blocks = 8192;
+    if (quads) blocks = (blocks + 7) / 8 * 8;  // zero_quads splits the grid by XCD
     (void)hipGetLastError();
     if (quads)
         hipLaunchKernelGGL(zero_quads, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
