@@ -45,7 +45,7 @@ struct PrologueArgs {
 template <int NJ>
 __global__ __launch_bounds__(256) void attn_prologue_kernel(PrologueArgs a) {
     constexpr int HD = 64 * NJ;
-    constexpr int RB = 32 / NJ;  // rows of one batch held in registers (32 VGPRs)
+    constexpr int RB = 24 / NJ;  // rows of one batch held in registers (24 VGPRs)
     __shared__ float cs_tab[HD / 2], sn_tab[HD / 2];
     __shared__ float row_s[4][HD];
     const int tok = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -65,11 +65,14 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(PrologueArgs a) {
         return a.v + (size_t)tok * kv_dim + (r - a.H - a.Hkv) * HD;
     };
 
-    // Everything this wave reads is requested up front: the gains, then its
-    // rows w, w + 4, ... (a batch of up to RB), and the loads are in flight
-    // while the angle table is built.  On gfx9 a store and a later load share
-    // one counter, so waiting on a load issued after a store waits for the
-    // store too; here each batch waits once, before its first store.
+    // The gains, then the wave's rows w, w + 4, ... (a batch of up to RB) are
+    // requested before any store, right after the angle table is built, so
+    // they are in flight across the table's barrier.  (Issued before the
+    // table, they kept 32 row registers live through its double-precision
+    // sincos: 110 VGPRs, 4 waves a SIMD, against 78 and 6 this way.)  On gfx9
+    // a store and a later load share one counter, so waiting on a load issued
+    // after a store waits for the store too; here each batch waits once,
+    // before its first store.
     float qg[NJ], kg[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) qg[j] = kg[j] = 1.f;
@@ -91,8 +94,6 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(PrologueArgs a) {
             }
         }
     };
-    load_batch(w);
-
     for (int i = tid; i < half; i += 256) {
         double theta = (double)pos;  // pos * s^i by the bits of i (i < 256)
 #pragma unroll
@@ -104,6 +105,7 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(PrologueArgs a) {
         cs_tab[i] = (float)c;
         sn_tab[i] = (float)s;
     }
+    load_batch(w);
     __syncthreads();
 
     // Rotation of dim d with its partner p (d + half below half, d - half
