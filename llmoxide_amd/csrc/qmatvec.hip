@@ -93,14 +93,14 @@ __device__ __forceinline__ float sbyte_f(uint32_t w, int i) { return (float)(int
 // quant.rs:33-47: 6-bit scale and min of sub-block j from the 12 packed
 // bytes held as three dwords.
 __device__ __forceinline__ void q4k_scale_min(const uint32_t (&s)[3], int j, float& sc, float& m) {
-    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xFF; };
-    if (j < 4) {
-        sc = (float)(byte(j) & 63);
-        m = (float)(byte(j + 4) & 63);
-    } else {
-        sc = (float)((byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4));
-        m = (float)((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
-    }
+    // With jl = j % 4, byte j (j < 4) or j + 4 ... lie at byte jl of the
+    // three dwords: B0 = bytes 0-3, B1 = 4-7, B2 = 8-11.  Selects, not a
+    // branch, so that callers' loads are not split by a divergent branch.
+    const int sh = 8 * (j & 3);
+    const uint32_t b0 = (s[0] >> sh) & 0xFF, b1 = (s[1] >> sh) & 0xFF, b2 = (s[2] >> sh) & 0xFF;
+    const bool lo = j < 4;
+    sc = (float)(lo ? b0 & 63 : (b2 & 0xF) | ((b0 >> 6) << 4));
+    m = (float)(lo ? b1 & 63 : (b2 >> 4) | ((b1 >> 6) << 4));
 }
 
 // The dot products of one unit of the RW rows with the T staged tokens,
@@ -118,18 +118,35 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[RW], int uw
         // to all rows, so only a step of x is live at a time.
         const int b = uw >> 2, p = uw & 3;
         const float* xc = xs + 64 * ux;
-        uint32_t q[RW][8];
+        uint32_t q[RW][8], hdr[RW][4];
         float a1[RW], c1[RW], a2[RW], c2[RW];
+        // every row's bytes requested before any is used
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             const uint8_t* blk = row[r] + (size_t)b * 144;
-            uint32_t hdr[4];
+            if constexpr (!LDS) {
+                // three 16-byte loads (blocks are 9 x 16 bytes; W is 16-byte aligned)
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 h4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(blk));
+                const u32x4 qa = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(blk + 16 + 32 * p));
+                const u32x4 qb = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(blk + 32 + 32 * p));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) hdr[i] = ld_u32<LDS>(blk + 4 * i);
+                for (int i = 0; i < 4; ++i) {
+                    hdr[r][i] = h4[i];
+                    q[r][i] = qa[i];
+                    q[r][4 + i] = qb[i];
+                }
+            } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) q[r][i] = ld_u32<LDS>(blk + 16 + 32 * p + 4 * i);
-            const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
-            const uint32_t sc3[3] = {hdr[1], hdr[2], hdr[3]};
+                for (int i = 0; i < 4; ++i) hdr[r][i] = ld_u32<LDS>(blk + 4 * i);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q[r][i] = ld_u32<LDS>(blk + 16 + 32 * p + 4 * i);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const float d = f16_lo(hdr[r][0]), dmin = f16_hi(hdr[r][0]);
+            const uint32_t sc3[3] = {hdr[r][1], hdr[r][2], hdr[r][3]};
             float sc1, m1, sc2, m2;
             q4k_scale_min(sc3, 2 * p, sc1, m1);
             q4k_scale_min(sc3, 2 * p + 1, sc2, m2);
@@ -336,15 +353,30 @@ __device__ __forceinline__ void unit_dot(const uint8_t* const (&row)[RW], int uw
     }
 }
 
+// x [n_tok, in_dim] into LDS, 16 bytes a thread a step, with four steps'
+// loads in flight before the first store: a load-then-store loop waits out a
+// full memory round trip per step (four at in_dim 4096).
+__device__ __forceinline__ void stage_x(float* xs, const float* x, int nx4, int tid) {
+    constexpr int U = 4, NT = kQmvWaves * 64;
+    const f32x4* src = reinterpret_cast<const f32x4*>(x);
+    f32x4* dst = reinterpret_cast<f32x4*>(xs);
+    int i = tid;
+    for (; i + (U - 1) * NT < nx4; i += U * NT) {  // all U steps in range: no branch between loads
+        f32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = src[i + u * NT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[i + u * NT] = v[u];
+    }
+    for (; i < nx4; i += NT) dst[i] = src[i];
+}
+
 template <int TY, int T>
 __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_kernel(QmvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float xs[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // stage x: n_tok * in_dim floats, 16 bytes per thread per step
-    const int nx4 = a.n_tok * a.in_dim / 4;
-    for (int i = tid; i < nx4; i += kQmvWaves * 64)
-        reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(a.x)[i];
+    stage_x(xs, a.x, a.n_tok * a.in_dim / 4, tid);
     __syncthreads();
 
     // Row groups of kQmvRows rows, dealt to the waves of all workgroups in
@@ -410,9 +442,7 @@ __global__ __launch_bounds__(kQmvWaves * 64) void qmatvec_lds_kernel(QmvArgs a) 
     static_assert((64 / UPG * GB + 15) / 16 + 1 <= NI * 64, "DMA instructions cover a chunk's window");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nx4 = a.n_tok * a.in_dim / 4;
-    for (int i = tid; i < nx4; i += kQmvWaves * 64)
-        reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(a.x)[i];
+    stage_x(xs, a.x, a.n_tok * a.in_dim / 4, tid);
     __syncthreads();
     uint8_t* slice = reinterpret_cast<uint8_t*>(xs + a.n_tok * a.in_dim) + wave * qmv_slice_bytes<TY>();
 
