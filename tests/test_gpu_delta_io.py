@@ -44,12 +44,15 @@ def test_front_matches_oracle(shape, t):
 @pytest.mark.parametrize("shape", [dict(conv_dim=384, key_dim=128, s_dim=64, kernel=4),
                                    dict(conv_dim=1280, key_dim=256, s_dim=128, kernel=3),
                                    dict(conv_dim=1536, key_dim=256, s_dim=128, kernel=6),
-                                   dict(conv_dim=2048, key_dim=512, s_dim=64, kernel=8)],
-                         ids=["two_channel", "one_wave_of_four", "k6_two_waves", "k8"])
+                                   dict(conv_dim=2048, key_dim=512, s_dim=64, kernel=8),
+                                   dict(conv_dim=1024, key_dim=256, s_dim=64, kernel=2),
+                                   dict(conv_dim=1792, key_dim=512, s_dim=128, kernel=5),
+                                   dict(conv_dim=768, key_dim=128, s_dim=64, kernel=7)],
+                         ids=["two_channel", "one_wave_of_four", "k6_two_waves", "k8", "k2", "k5", "k7"])
 def test_front_block_edges(shape, t):
-    """conv_dim % 256 == 128 takes the two-channel kernel; the others stream
-    with a last workgroup only partly inside conv_dim, q/k and v channels in
-    one wave, a full segment then a ragged one, and kernels up to 8 taps."""
+    """16-byte form at conv widths 2-8, with q/k and v channels in one wave and
+    both interior and edge token chunks; in the first case (conv_dim % 256 ==
+    128) the last 256-channel block is only half inside conv_dim."""
     say(f"delta front edges {shape} t={t}")
     x, taps, state = front_inputs(shape, t, 11)
     kw = dict(key_dim=shape["key_dim"], s_dim=shape["s_dim"])
