@@ -20,6 +20,14 @@ CONFIGS = {
     # the smallest and largest head sizes the path takes, with partial rope on the latter
     "hd64": dict(n_heads=4, n_kv_heads=2, head_dim=64, n_rot=64, rope_base=1e4, q_stride=64),
     "hd512_partial": dict(n_heads=2, n_kv_heads=1, head_dim=512, n_rot=128, rope_base=1e6, q_stride=512),
+    # more rows a wave than one register batch holds (the GPU kernel loads a
+    # wave's rows in batches of 24 / (head_dim / 64)): two or more batches
+    "many_heads_hd64": dict(n_heads=64, n_kv_heads=32, head_dim=64, n_rot=64, rope_base=1e4, q_stride=64),
+    "many_heads_hd128": dict(n_heads=40, n_kv_heads=8, head_dim=128, n_rot=128, rope_base=1e6, q_stride=128),
+    "gemma_c4": dict(n_heads=16, n_kv_heads=8, head_dim=256, n_rot=256, rope_base=1e4, q_stride=256,
+                     v_norm=True),
+    "gemma4_global": dict(n_heads=16, n_kv_heads=1, head_dim=512, n_rot=128, rope_base=1e6, q_stride=512,
+                          v_norm=True),
 }
 
 
