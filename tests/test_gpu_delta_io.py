@@ -64,6 +64,32 @@ def test_front_block_edges(shape, t):
     np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)
 
 
+@pytest.mark.parametrize("t", [1, 3, 6, 9])
+@pytest.mark.parametrize("offset", [0, 1], ids=["16byte", "two_channel"])
+@pytest.mark.parametrize("shape", [dict(conv_dim=2048, key_dim=512, s_dim=64, kernel=8),
+                                   dict(conv_dim=640, key_dim=128, s_dim=64, kernel=8)],
+                         ids=["k8_c2048", "k8_c640"])
+def test_front_batches_shorter_than_the_window(shape, offset, t):
+    """Seven window rows and batches of 1-9 tokens: outputs mix old window rows
+    and batch rows, and the new window mixes both too (t < 7). x placed
+    `offset` floats past a 16-byte boundary picks the form (0: 16-byte,
+    1: two-channel); c640 ends in a half-filled 256-channel block."""
+    say(f"delta front short batch {shape} offset={offset} t={t}")
+    x, taps, state = front_inputs(shape, t, 40 + t)
+    kw = dict(key_dim=shape["key_dim"], s_dim=shape["s_dim"])
+    ref, st_ref = oracle.delta_front(x, taps, state, **kw)
+    n = t * shape["conv_dim"]
+    flat = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    xd = flat[offset:offset + n].view(t, shape["conv_dim"])
+    xd.copy_(dev(x))
+    assert xd.data_ptr() % 16 == 4 * offset
+    sd = dev(state)
+    out = lmx.delta_front(xd, dev(taps), sd, **kw)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, abs_tol=1e-5, rel_tol=1e-5, what="conv_out")
+    np.testing.assert_array_equal(sd.cpu().numpy(), st_ref)
+
+
 def test_front_unaligned_input_takes_the_two_channel_form():
     """x 4 bytes off a 16-byte boundary: the two-channel kernel runs. Both forms
     meet the oracle; they sum the head norm in different orders, so their
