@@ -179,7 +179,8 @@ static lmx_status scratch_of_stream_device(hipStream_t stream, void** out) {
 }
 
 // ---- tuning overrides (see Tuning in common.hpp)
-static std::atomic<int> g_tune_kernel{-1}, g_tune_gp{0}, g_tune_kh{-1}, g_tune_krows{-1}, g_tune_mh{-1};
+static std::atomic<int> g_tune_kernel{-1}, g_tune_gp{0}, g_tune_kh{-1}, g_tune_krows{-1}, g_tune_mh{-1},
+    g_tune_dfused{-1};
 static std::once_flag g_tune_once;
 
 static void read_tuning_env() {
@@ -198,11 +199,14 @@ static void read_tuning_env() {
     g_tune_krows.store(choice("LMX_DECODE_KROWS", "1", 1, "0", 0));
     const char* mh = std::getenv("LMX_DECODE_MH");
     g_tune_mh.store(mh && mh[0] == '0' ? 0 : -1);
+    const char* df = std::getenv("LMX_DELTA_FUSED");
+    g_tune_dfused.store(df && df[0] == '0' ? 0 : -1);
 }
 
 Tuning tuning() {
     std::call_once(g_tune_once, read_tuning_env);
-    return Tuning{g_tune_kernel.load(), g_tune_gp.load(), g_tune_kh.load(), g_tune_krows.load(), g_tune_mh.load()};
+    return Tuning{g_tune_kernel.load(), g_tune_gp.load(), g_tune_kh.load(), g_tune_krows.load(), g_tune_mh.load(),
+                  g_tune_dfused.load()};
 }
 
 }  // namespace lmx

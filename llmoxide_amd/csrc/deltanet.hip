@@ -11,6 +11,8 @@
 // Per token and row j (qwen35/cpu.rs:228-244, term for term):
 //   S_j <- g S_j;  pred = S_j . k;  d = b (v_j - pred);  S_j += d k;
 //   o_j = scale * (S_j . q)
+#include <atomic>
+
 #include "common.hpp"
 
 namespace lmx {
@@ -250,6 +252,50 @@ struct ChunkSmem {
     static constexpr int LD = C + 4;  // row stride in floats; keeps float4 rows aligned
 };
 
+// LDS of the prep: the K/Q staging rows or the A, T, P work matrices (the
+// same space, in turn), then the decays and b, one copy per wave.
+template <int SD, int C>
+struct PrepLds {
+    static constexpr int LD = ChunkSmem<C>::LD, KLD = SD + 4;
+    static constexpr int STAGE = 2 * C * KLD, WORK = 3 * C * LD;
+    static constexpr int MAIN = STAGE > WORK ? STAGE : WORK;
+    static constexpr int FLOATS = MAIN + 2 * 4 * 64;
+};
+
+// Stores of what the scan reads, in the one-launch form.  Each XCD has its
+// own L2: a plain store stays in the writer's L2 until the launch ends, so it
+// is seen only by workgroups on the writer's XCD; an agent-scope store (sc1)
+// writes through to memory, where a workgroup on another XCD that has not yet
+// read the line finds it.  The 16-byte agent form is two 8-byte atomic stores
+// that the compiler emits itself (an asm store is opaque to its hazard and
+// wait tracking).
+__device__ __forceinline__ void st16_agent(uint8_t* p, bf16x8 v) {
+    uint64_t u[2];
+    __builtin_memcpy(u, &v, 16);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), u[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, u[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_piece_m(uint8_t* p, int lane, const Bf8& v, bool agent) {
+    if (agent) {
+        st16_agent(p + 16 * lane, v.hi);
+        st16_agent(p + 1024 + 16 * lane, v.lo);
+    } else {
+        st_piece(p, lane, v);
+    }
+}
+__device__ __forceinline__ void st_f32_m(float* p, float v, bool agent) {
+    if (agent)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+// The XCD (accelerator complex die) this wave runs on.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 15;
+}
+
 // One workgroup per (chunk, k-head).  K K^T and Q K^T are shared by the v-heads
 // hv = hk + u * n_kh (hv % n_kh == hk, deltanet.wgsl:200), so they are formed
 // once, into registers, from K and Q rows staged in LDS with whole-line loads;
@@ -260,38 +306,48 @@ struct ChunkSmem {
 // chunk's K and Q rows are written once more, split, in the scan's operand
 // order for X and Y to ws_K, so the 16 scan workgroups that read a k-head's
 // chunk split nothing themselves (the scan forms K^T from its K tiles in LDS).
-template <int SD, int C, bool SPLIT>
-__global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
-                                                               float* ws_P, float* ws_e,
-                                                               uint8_t* ws_K, int n_chunks) {
+//
+// The workgroup walks items first, first + stride, ...  FUSED (inside
+// delta_chunk_fused_kernel): items are numbered chunk-major (chunk ch, k-head
+// hk is item ch n_kh + hk) so that early chunks are done first, and once an
+// item is complete its flag flags[item] is set to 1.  Scan workgroup j records
+// its XCD as reg[j] = XCD + 1 (reg follows the flags and the error word): an
+// item's stores stay plain only when every scan workgroup that reads them has
+// registered on this workgroup's XCD, and are agent-scope otherwise, so the
+// result never depends on where workgroups run.  Otherwise items are numbered
+// k-head-major and the stores are plain.
+template <int SD, int C, bool SPLIT, bool FUSED>
+__device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T, float* ws_P,
+                                                float* ws_e, uint8_t* ws_K, int n_chunks,
+                                                int first, int stride, float* lds,
+                                                uint32_t* flags) {
     constexpr int NM = C / 16, LD = ChunkSmem<C>::LD;
     constexpr int NTILE = NM * (NM + 1) / 2, TPW = (NTILE + 3) / 4;
-    constexpr int KLD = SD + 4;            // staged K/Q row stride in floats
-    constexpr int STAGE = 2 * C * KLD;     // K and Q rows of the chunk
-    constexpr int WORK = 3 * C * LD;       // A, T, P
-    __shared__ __attribute__((aligned(16))) float smem[STAGE > WORK ? STAGE : WORK];
-    float* const Ks = smem;
-    float* const Qs = smem + C * KLD;
-    float* const As = smem;               // strictly lower A, later M
-    float* const Tm = smem + C * LD;      // (I + A)^-1
-    float* const Ps = smem + 2 * C * LD;  // P
-    __shared__ __attribute__((aligned(16))) float lg_w[4][64];  // one copy per wave
-    __shared__ __attribute__((aligned(16))) float b_w[4][64];
+    constexpr int KLD = PrepLds<SD, C>::KLD;  // staged K/Q row stride in floats
+    float* const Ks = lds;
+    float* const Qs = lds + C * KLD;
+    float* const As = lds;               // strictly lower A, later M
+    float* const Tm = lds + C * LD;      // (I + A)^-1
+    float* const Ps = lds + 2 * C * LD;  // P
+    float (*const lg_w)[64] = reinterpret_cast<float (*)[64]>(lds + PrepLds<SD, C>::MAIN);
+    float (*const b_w)[64] = lg_w + 4;
     const int tid = threadIdx.x;
     const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-    // Items (chunk, k-head) blockIdx.x, + gridDim.x, ... (two workgroups a
-    // CU): the next item's K and Q rows load into registers while this one is
+    // Items first, first + stride, ... (two workgroups a CU in the prep
+    // kernel): the next item's K and Q rows load into registers while this one is
     // worked, so only a workgroup's first staging waits on memory (staging
     // was a third of a workgroup's time, all of them loading at once).
     // Rows past the end of the batch are zero.
     constexpr int SJ = C * SD / 4 / 256;
     f32x4 rq[SJ], rk[SJ];
     const int n_items = n_chunks * a.n_kh;
+    auto item_ch = [&](int item) { return FUSED ? item / a.n_kh : item % n_chunks; };
+    auto item_hk = [&](int item) { return FUSED ? item % a.n_kh : item / n_chunks; };
     auto load_rows = [&](int item) {
-        const int lc0 = (item % n_chunks) * C, lnv = min(C, a.n_tok - lc0), lhk = item / n_chunks;
+        const int lc0 = item_ch(item) * C, lnv = min(C, a.n_tok - lc0), lhk = item_hk(item);
 #pragma unroll
         for (int j = 0; j < SJ; ++j) {
             const int idx = tid + 256 * j, row = idx / (SD / 4), c4 = idx % (SD / 4);
@@ -305,10 +361,23 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
             rk[j] = k;
         }
     };
-    if ((int)blockIdx.x < n_items) load_rows(blockIdx.x);
-    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const int ch = item % n_chunks, hk = item / n_chunks;
+    if (first < n_items) load_rows(first);
+    const uint32_t my_xcc = FUSED ? xcc_id() : 0;
+    const uint32_t* const reg = FUSED ? flags + n_items + 1 : nullptr;
+    for (int item = first; item < n_items; item += stride) {
+        const int ch = item_ch(item), hk = item_hk(item);
         const int c0 = ch * C, nv = min(C, a.n_tok - c0);
+        // FUSED: the registrations of this item's readers (v-heads hk + u n_kh,
+        // every row block), checked at the staging barrier below
+        int here = 1;
+        if constexpr (FUSED) {
+            const int per = a.n_vh / a.n_kh, n_rd = per * (SD / 16);
+            for (int r = tid; r < n_rd; r += 256) {
+                const int hv = hk + (r % per) * a.n_kh, rb = r / per;
+                here &= __hip_atomic_load(reg + rb * a.n_vh + hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        my_xcc + 1;
+            }
+        }
 
         // alpha and beta of the next v-head, in flight during the work before it
         float al_n = 0.f, be_n = 0.f;
@@ -329,8 +398,12 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
             *reinterpret_cast<f32x4*>(Qs + row * KLD + 4 * c4) = rq[j];
             *reinterpret_cast<f32x4*>(Ks + row * KLD + 4 * c4) = rk[j];
         }
-        __syncthreads();
-        if (item + (int)gridDim.x < n_items) load_rows(item + gridDim.x);
+        bool agent = false;  // this item's stores write through (see above)
+        if constexpr (FUSED)
+            agent = __builtin_amdgcn_readfirstlane(__syncthreads_and(here)) == 0;
+        else
+            __syncthreads();
+        if (item + stride < n_items) load_rows(item + stride);
 
         // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
         // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
@@ -371,9 +444,9 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
             for (int q = tid; q < NM * SX * 64; q += 256) {
                 const int l = q & 63, pc = q >> 6, m = pc / SX, sg = pc % SX;
                 const int t = 16 * m + (l & 15), c0 = 32 * sg + 4 * (l >> 4);
-                st_piece(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)));
-                st_piece(kb + C * SD * 4 + pc * kPiece, l,
-                         split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)));
+                st_piece_m(kb + pc * kPiece, l, split8(ld4(Ks + t * KLD + c0), ld4(Ks + t * KLD + c0 + 16)), agent);
+                st_piece_m(kb + C * SD * 4 + pc * kPiece, l,
+                           split8(ld4(Qs + t * KLD + c0), ld4(Qs + t * KLD + c0 + 16)), agent);
             }
         }
 
@@ -398,8 +471,8 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
                 b_w[w][lane] = b;
                 if (w == 0 && lane < C) {
                     const float lgC = __shfl(l, C - 1);
-                    ws_e[cb * 2 * C + lane] = fast_exp2(l);
-                    ws_e[cb * 2 * C + C + lane] = fast_exp2(lgC - l);
+                    st_f32_m(ws_e + cb * 2 * C + lane, fast_exp2(l), agent);
+                    st_f32_m(ws_e + cb * 2 * C + C + lane, fast_exp2(lgC - l), agent);
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -497,8 +570,8 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
                             mo[hf][e] = bn <= bm ? mv[e] : 0.f;
                         }
                     }
-                    st_piece(Tg + pc * kPiece, l, split8(to[0], to[1]));
-                    st_piece(Mg + pc * kPiece, l, split8(mo[0], mo[1]));
+                    st_piece_m(Tg + pc * kPiece, l, split8(to[0], to[1]), agent);
+                    st_piece_m(Mg + pc * kPiece, l, split8(mo[0], mo[1]), agent);
                 }
                 continue;
             }
@@ -523,7 +596,22 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
                 *reinterpret_cast<f32x4*>(Mg + 4 * q) = mo;
             }
         }
+        if constexpr (FUSED) {
+            // Every thread's stores of the item acknowledged, then the flag.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(flags + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+}
+
+template <int SD, int C, bool SPLIT>
+__global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, float* ws_T,
+                                                               float* ws_P, float* ws_e,
+                                                               uint8_t* ws_K, int n_chunks) {
+    __shared__ __attribute__((aligned(16))) float lds[PrepLds<SD, C>::FLOATS];
+    chunk_prep_body<SD, C, SPLIT, false>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, blockIdx.x, gridDim.x,
+                                         lds, nullptr);
 }
 
 // One workgroup per (v-head, 16 state rows); blockIdx % n_vh == hv, so with
@@ -749,24 +837,47 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(DeltaArgs a, cons
 // and lane L receives tokens t0 .. t0 + 3 of dim 16 ct + L.  That saves a
 // third of the K/Q piece bytes the prep writes and a quarter of the pieces
 // each scan workgroup reads from L2 per chunk.
+//
+// LDS: the Z, W and state tiles (bf16 hi/lo, D layout), then Kth and Ktl.
 template <int SD, int C>
-__global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, const uint8_t* ws_T,
-                                                                  const uint8_t* ws_P,
-                                                                  const float* ws_e,
-                                                                  const uint8_t* ws_K, int n_chunks) {
+struct ScanLds {
+    static constexpr int NT = SD / 16, NM = C / 16, KTLD = SD + 4;  // Kth/Ktl row stride (bf16)
+    static constexpr int TILES = (4 * NM + 2 * NT) * 64;           // bf16x4 entries
+    static constexpr int BYTES = TILES * 8 + 2 * C * KTLD * 2;
+};
+
+// A wait for a ready flag gives up after this many polls (about 2^16 x 2 us
+// at the box's clock), records the failure in *err and lets the workgroup
+// finish, so no launch can hang on a producer that never runs.
+constexpr uint32_t kFlagPolls = 1u << 16;
+
+// blk: the workgroup's (v-head, row block) index.  FUSED: the workgroup
+// first records its XCD at err[1 + blk] (see chunk_prep_body); chunk ch's
+// inputs of its k-head are ready once flags[ch n_kh + hk] is 1, and the flag
+// of the chunk after next is polled a chunk ahead, so a producer that keeps
+// ahead costs no round trip on the chain.
+template <int SD, int C, bool FUSED>
+__device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uint8_t* ws_T,
+                                                   const uint8_t* ws_P, const float* ws_e,
+                                                   const uint8_t* ws_K, int n_chunks, int blk,
+                                                   uint8_t* lds, const uint32_t* flags,
+                                                   uint32_t* err) {
     constexpr int NT = SD / 16, NM = C / 16, TPW = NT / 4;
     constexpr int SX = SD / 32, SC = C / 32;  // 32-wide steps over dims, over tokens
     constexpr size_t KQB = (size_t)2 * C * SD * 4;  // ws_K bytes per (chunk, k-head)
     static_assert(NM % 2 == 0 && NT % 4 == 0, "whole 32-wide steps, whole column tiles per wave");
-    __shared__ bf16x4 Zh[NM * 64], Zl[NM * 64];  // Z tiles, D layout
-    __shared__ bf16x4 Wh[NM * 64], Wl[NM * 64];  // W tiles, D layout
-    __shared__ bf16x4 Sh[NT * 64], Sl[NT * 64];  // state columns, D layout
-    constexpr int KTLD = SD + 4;                   // Kth/Ktl row stride (bf16), 8-byte rows
-    __shared__ __attribute__((aligned(16))) __bf16 Kth[C][KTLD];
-    __shared__ __attribute__((aligned(16))) __bf16 Ktl[C][KTLD];
+    bf16x4* const Zh = reinterpret_cast<bf16x4*>(lds);  // Z tiles, D layout
+    bf16x4* const Zl = Zh + NM * 64;
+    bf16x4* const Wh = Zl + NM * 64;  // W tiles, D layout
+    bf16x4* const Wl = Wh + NM * 64;
+    bf16x4* const Sh = Wl + NM * 64;  // state columns, D layout
+    bf16x4* const Sl = Sh + NT * 64;
+    constexpr int KTLD = ScanLds<SD, C>::KTLD;  // 8-byte rows
+    __bf16 (*const Kth)[KTLD] = reinterpret_cast<__bf16 (*)[KTLD]>(Sl + NT * 64);
+    __bf16 (*const Ktl)[KTLD] = Kth + C;
     const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hv = blockIdx.x % a.n_vh, rb = blockIdx.x / a.n_vh;
+    const int hv = blk % a.n_vh, rb = blk / a.n_vh;
     const int row0 = rb * 16, hk = hv % a.n_kh;
     const bool tok_wave = NM >= 4 || w < NM;
     const int m = tok_wave ? w : 0;
@@ -833,6 +944,22 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
     struct Small {
         f32x4 v, e, wo;  // V, exp(lg), exp(lg_C - lg) at tokens 16 m + 4 lq + r
         float gam;       // exp(lg_C)
+        uint32_t rdy;    // FUSED: the flag of the chunk after this one, as polled
+    };
+    // FUSED: flag polls, and the bounded wait (after one failure the
+    // workgroup waits no more).
+    bool failed = false;
+    auto poll = [&](int c) -> uint32_t {
+        return __hip_atomic_load(flags + (size_t)c * a.n_kh + hk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto wait_ready = [&](int c) {
+        for (uint32_t n = 0; !failed && __builtin_amdgcn_readfirstlane(poll(c)) == 0; ++n) {
+            if (n == kFlagPolls) {
+                failed = true;
+                if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __builtin_amdgcn_s_sleep(32);
+        }
     };
     // Tokens past the end of the last chunk read row 0 of the chunk instead:
     // their b is 0, so their rows and columns of Tb are exactly zero and so
@@ -855,6 +982,11 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
     auto step = [&](int ch, const Small& cur, Small& nxt) {
         const int nv = a.n_tok - ch * C;
         const int cn = min(ch + 1, n_chunks - 1);
+        if constexpr (FUSED) {
+            if (__builtin_amdgcn_readfirstlane(cur.rdy) == 0) wait_ready(cn);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);  // chunk cn's loads stay after the wait
+            nxt.rdy = poll(min(cn + 1, n_chunks - 1));
+        }
         fetch_small(cn, nxt);
         f32x4 X = z4, Y = z4;
         if (tok_wave) {
@@ -932,6 +1064,12 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
     // Chunk 0's inputs, drained before the loop so the waits inside it follow
     // the loop body's own issue order.
     Small in0, in1;
+    if constexpr (FUSED) {
+        if (threadIdx.x == 0) __hip_atomic_store(err + 1 + blk, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_ready(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        in0.rdy = poll(min(1, n_chunks - 1));
+    }
     fetch_small(0, in0);
     if (tok_wave) {
 #pragma unroll
@@ -959,27 +1097,108 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
     for (int jj = 0; jj < TPW; ++jj) *reinterpret_cast<f32x4*>(srow + 16 * (TPW * w + jj)) = Sown[jj];
 }
 
+template <int SD, int C>
+__global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, const uint8_t* ws_T,
+                                                                  const uint8_t* ws_P,
+                                                                  const float* ws_e,
+                                                                  const uint8_t* ws_K, int n_chunks) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[ScanLds<SD, C>::BYTES];
+    chunk_scan_bf_body<SD, C, false>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, blockIdx.x, lds, nullptr, nullptr);
+}
+
+// Prep and scan in one launch (chunks of 32 and 64).  Workgroups [0, n_prep)
+// run the prep over items b, b + n_prep, ... in chunk order and publish each
+// item's flag; workgroups [n_prep, n_prep + n_vh SD / 16) run the scan, each
+// waiting for a chunk's flag before it loads that chunk's inputs.  Prep
+// workgroups never wait and come first in dispatch order, and the host
+// launches this form only when the GPU holds more workgroups than the scan
+// has, so a prep workgroup can always run.  Two workgroups a CU: the scan's
+// chains leave most issue cycles idle, and the prep fills them.
+template <int SD, int C>
+__global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, float* ws_T, float* ws_P,
+                                                                   float* ws_e, uint8_t* ws_K,
+                                                                   int n_chunks, int n_prep,
+                                                                   uint32_t* flags, uint32_t* err) {
+    constexpr int PB = PrepLds<SD, C>::FLOATS * 4, SB = ScanLds<SD, C>::BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[PB > SB ? PB : SB];
+    const int b = blockIdx.x;
+    if (b < n_prep)
+        chunk_prep_body<SD, C, true, true>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, b, n_prep,
+                                           reinterpret_cast<float*>(lds), flags);
+    else
+        chunk_scan_bf_body<SD, C, true>(a, reinterpret_cast<const uint8_t*>(ws_T),
+                                        reinterpret_cast<const uint8_t*>(ws_P), ws_e, ws_K, n_chunks,
+                                        b - n_prep, lds, flags, err);
+}
+
+// Clears the one-launch form's flags, error word and registrations (a kernel,
+// not a memset, so the call may sit in a captured graph).
+__global__ __launch_bounds__(256) void delta_flags_clear_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
 // Workspace: Tb and M [n_vh][n_chunks][chunk^2] floats (fp32 fragments, or
 // split-bf16 pieces of the same size), the decays [n_vh][n_chunks][2 chunk],
 // and, for the split path (chunks of 32 and 64), K and Q pieces
-// [n_chunks][n_kh][2 chunk s_dim] floats' worth.
+// [n_chunks][n_kh][2 chunk s_dim] floats' worth, then the one-launch form's
+// ready flags [n_chunks][n_kh], its error word and the scan workgroups' XCD
+// registrations [n_vh s_dim / 16].
 static bool chunk_split(int chunk) { return chunk >= 32; }
 
 static size_t chunk_ws_floats(const lmx_dop* op, int chunk) {
     const size_t n_chunks = (op->n_tok + chunk - 1) / chunk;
-    const size_t kq = chunk_split(chunk) ? (size_t)op->n_kh * n_chunks * 2 * chunk * op->s_dim : 0;
-    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk) + kq;
+    const bool split = chunk_split(chunk);
+    const size_t kq = split ? (size_t)op->n_kh * n_chunks * 2 * chunk * op->s_dim : 0;
+    const size_t fl = split ? (size_t)op->n_kh * n_chunks + 1 + (size_t)op->n_vh * (op->s_dim / 16) : 0;
+    return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk) + kq + fl;
 }
 
 size_t deltanet_chunked_ws(const lmx_dop* op, int chunk) {
     return (chunk_ws_floats(op, chunk) * 4 + 255) / 256 * 256;
 }
 
+// Workgroups of delta_chunk_fused_kernel the current GPU holds at once
+// (occupancy x CUs), 0 if unknown; cached per device.
+template <int SD, int C>
+static int fused_slots() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v != 0) return v > 0 ? v : 0;
+    int per_cu = 0, n_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&delta_chunk_fused_kernel<SD, C>), 256, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        per_cu = n_cu = 0;
+    v = per_cu * n_cu;
+    cache[dev].store(v > 0 ? v : -1, std::memory_order_relaxed);
+    return v > 0 ? v : 0;
+}
+
 template <int SD, int C>
 static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks, float* wsT,
-                           float* wsP, float* wsE, uint8_t* wsK, hipStream_t st) {
+                           float* wsP, float* wsE, uint8_t* wsK, uint32_t* wsF, hipStream_t st) {
     constexpr bool SPLIT = C >= 32;
     const int n_items = n_chunks * n_kh;
+    if constexpr (SPLIT) {
+        // One launch when the GPU holds more workgroups than the scan has, so
+        // that a prep workgroup can always run.  Prep workgroups: what the GPU
+        // holds beside the scan, a multiple of 8 so that scan workgroup j
+        // still runs on XCD j % 8 with the other row blocks of its v-head.
+        const int n_scan = n_vh * (SD / 16);
+        const int slots = tuning().delta_fused == 0 ? 0 : fused_slots<SD, C>();
+        if (slots > n_scan) {
+            int n_prep = std::min(n_items, slots - n_scan);
+            if (n_prep >= 8) n_prep &= ~7;
+            const int n_words = n_items + 1 + n_scan;  // flags, error word, registrations
+            hipLaunchKernelGGL(delta_flags_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, st,
+                               wsF, n_words);
+            hipLaunchKernelGGL((delta_chunk_fused_kernel<SD, C>), dim3(n_prep + n_scan), dim3(256), 0, st, a,
+                               wsT, wsP, wsE, wsK, n_chunks, n_prep, wsF, wsF + n_items);
+            return;
+        }
+    }
     hipLaunchKernelGGL((delta_chunk_prep_kernel<SD, C, SPLIT>), dim3(std::min(n_items, 2 * 256)), dim3(256), 0, st,
                        a, wsT, wsP, wsE, wsK, n_chunks);
     if constexpr (SPLIT)
@@ -1004,10 +1223,12 @@ lmx_status deltanet_chunked(const lmx_dop* op, const float* ssm_a, const float* 
     float* wsE = wsP + per * chunk * chunk;
     uint8_t* wsK = reinterpret_cast<uint8_t*>(wsE + per * 2 * chunk);
     const int sd = (int)op->s_dim;
+    uint32_t* wsF = reinterpret_cast<uint32_t*>(
+        wsK + (chunk_split(chunk) ? (size_t)op->n_kh * n_chunks * 2 * chunk * sd * 4 : 0));
     (void)hipGetLastError();
 #define LMX_CH(SDV, CV)                                                                          \
     if (sd == SDV && chunk == CV) {                                                              \
-        launch_chunked<SDV, CV>(a, (int)op->n_vh, (int)op->n_kh, n_chunks, wsT, wsP, wsE, wsK, st); \
+        launch_chunked<SDV, CV>(a, (int)op->n_vh, (int)op->n_kh, n_chunks, wsT, wsP, wsE, wsK, wsF, st); \
         LMX_CHECK_LAUNCH();                                                                      \
         return LMX_OK;                                                                           \
     }

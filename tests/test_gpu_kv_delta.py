@@ -1,5 +1,6 @@
 """GPU parity: KV append (bit-exact f16 rows and slots), the token-sequential
 and chunked delta rule, and ragged multi-sequence decode."""
+import ctypes
 import sys
 
 import numpy as np
@@ -154,6 +155,41 @@ def test_delta_chunked_c5_full_size_matches_sequential_kernel():
     e_o = assert_close(o_chk, o_seq, what="o")
     e_s = assert_close(S_chk, S_seq, what="S")
     say(f"  o max_abs={e_o[0]:.2e} rel={e_o[1]:.2e}; S max_abs={e_s[0]:.2e} rel={e_s[1]:.2e}")
+
+
+@pytest.mark.parametrize("T,n_vh,n_kh,sd,chunk", [(4096, 32, 16, 128, 64), (2577, 32, 16, 128, 64),
+                                                  (250, 8, 4, 64, 32), (99, 4, 2, 128, 32),
+                                                  (37, 4, 2, 64, 64)])
+def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_env):
+    """The one-launch form (prep workgroups publish a ready flag per (chunk,
+    k-head); scan workgroups wait for it) against prep and scan as two
+    launches (LMX_DELTA_FUSED=0).  Each item and chunk runs the same
+    arithmetic, so o and the state are bit-identical.  The workspace is
+    filled with 0x5A bytes before each call, so its flags start nonzero: the
+    call itself must clear them, and it leaves the error word (a wait that
+    gave up) at 0; the two-launch form does not touch it."""
+    say(f"delta_chunked one launch vs two T={T} n_vh={n_vh} n_kh={n_kh} sd={sd} chunk={chunk}")
+    conv, al, be, S0, A, dt = delta_inputs(T + 5, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.1)
+    n_ch = -(-T // chunk)
+    err_at = 4 * (n_vh * n_ch * (2 * chunk * chunk + 2 * chunk) + n_kh * n_ch * 2 * chunk * sd + n_kh * n_ch)
+    op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    ws = lmx.Workspace(lmx.lib().lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk),
+                       device=torch.device("cuda"))
+    base = ws.base - ws.buf.data_ptr()
+    runs = {}
+    for fused in ("1", "0"):
+        tuning_env("LMX_DELTA_FUSED", fused)
+        ws.buf.fill_(0x5A)
+        state = dev(S0.copy())
+        out = lmx.delta_chunked(dev(conv), dev(al), dev(be), state, dev(A), dev(dt), n_vh=n_vh, n_kh=n_kh,
+                                s_dim=sd, chunk=chunk, workspace=ws)
+        torch.cuda.synchronize()
+        err = int(ws.buf[base + err_at:base + err_at + 4].cpu().numpy().view(np.uint32)[0])
+        runs[fused] = (out.cpu().numpy(), state.cpu().numpy(), err)
+    assert runs["1"][2] == 0, "a scan workgroup gave up waiting for a ready flag"
+    assert runs["0"][2] == 0x5A5A5A5A
+    np.testing.assert_array_equal(runs["1"][0], runs["0"][0])
+    np.testing.assert_array_equal(runs["1"][1], runs["0"][1])
 
 
 @pytest.mark.parametrize("T", [2577, 6400])
