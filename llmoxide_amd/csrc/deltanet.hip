@@ -367,21 +367,13 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
     for (int item = first; item < n_items; item += stride) {
         const int ch = item_ch(item), hk = item_hk(item);
         const int c0 = ch * C, nv = min(C, a.n_tok - c0);
-        // FUSED: the registrations of this item's readers (v-heads hk + u n_kh,
-        // every row block), checked at the staging barrier below
-        int here = 1;
-        if constexpr (FUSED) {
-            const int per = a.n_vh / a.n_kh, n_rd = per * (SD / 16);
-            for (int r = tid; r < n_rd; r += 256) {
-                const int hv = hk + (r % per) * a.n_kh, rb = r / per;
-                here &= __hip_atomic_load(reg + rb * a.n_vh + hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                        my_xcc + 1;
-            }
-        }
 
         // alpha and beta of the next v-head, in flight during the work before it
-        float al_n = 0.f, be_n = 0.f;
+        // (and its ssm_a, dt_bias)
+        float al_n = 0.f, be_n = 0.f, sa_n, dtb_n;
         auto ab_fetch = [&](int hv) {
+            sa_n = a.ssm_a[hv];
+            dtb_n = a.dt_bias[hv];
             if (lane < nv) {
                 const size_t gi = (size_t)(c0 + lane) * a.n_vh + hv;
                 al_n = a.alpha[gi];
@@ -398,15 +390,34 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             *reinterpret_cast<f32x4*>(Qs + row * KLD + 4 * c4) = rq[j];
             *reinterpret_cast<f32x4*>(Ks + row * KLD + 4 * c4) = rk[j];
         }
-        bool agent = false;  // this item's stores write through (see above)
-        if constexpr (FUSED)
-            agent = __builtin_amdgcn_readfirstlane(__syncthreads_and(here)) == 0;
-        else
-            __syncthreads();
-        if (item + stride < n_items) load_rows(item + stride);
+        __syncthreads();
+        // FUSED: the registrations of this item's readers (v-heads hk + u n_kh,
+        // every row block), combined after the Gram tiles, so their round trip
+        // is hidden; issued before the row prefetch, so that wait does not
+        // cover it.  A registration, once made, never changes, so a reader
+        // seen on this XCD here is there for good.
+        int here = 1;
+        if constexpr (FUSED) {
+            const int per = a.n_vh / a.n_kh, n_rd = per * (SD / 16);
+            for (int r = tid; r < n_rd; r += 256) {
+                const int hv = hk + (r % per) * a.n_kh, rb = r / per;
+                here &= __hip_atomic_load(reg + rb * a.n_vh + hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        my_xcc + 1;
+            }
+        }
+        // The next item's rows.  FUSED issues them once this item is
+        // published: beside the scan, issuing them stalls the wave for microseconds,
+        // and an item's latency matters only for the first chunks, which the
+        // scan waits for; later items have time to spare.
+        const bool more = item + stride < n_items;
+        if (!FUSED && more) load_rows(item + stride);
 
         // Gram tiles (m, n), n <= m, dealt round-robin to the 4 waves; a tile's
-        // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.
+        // D layout is lane (column 16 n + lr), rows 16 m + 4 lq + r.  SPLIT:
+        // split-bf16 triples over 32-wide dim steps (the operands of both
+        // tiles are rows of K or Q, in the same slot order), a fifth of the
+        // matrix-core time of the fp32 steps, which matters most beside the
+        // scan's chains in the one-launch form.
         f32x4 gk[TPW], gq[TPW];
         int tile_m[TPW], tile_n[TPW];
 #pragma unroll
@@ -424,16 +435,30 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             const float* km = Ks + (16 * m + lr) * KLD + 4 * lq;
             const float* qm = Qs + (16 * m + lr) * KLD + 4 * lq;
             const float* kn = Ks + (16 * n + lr) * KLD + 4 * lq;
+            if constexpr (SPLIT) {
 #pragma unroll
-            for (int u = 0; u < SD / 16; ++u) {
-                const f32x4 a4 = ld4(km + 16 * u), q4 = ld4(qm + 16 * u), b4 = ld4(kn + 16 * u);
+                for (int sg = 0; sg < SD / 32; ++sg) {
+                    const Bf8 ka = split8(ld4(km + 32 * sg), ld4(km + 32 * sg + 16));
+                    const Bf8 qa = split8(ld4(qm + 32 * sg), ld4(qm + 32 * sg + 16));
+                    const Bf8 kb = split8(ld4(kn + 32 * sg), ld4(kn + 32 * sg + 16));
+                    gk[k] = mfma3(ka, kb, gk[k]);
+                    gq[k] = mfma3(qa, kb, gq[k]);
+                }
+            } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    gk[k] = mfma4(a4[r], b4[r], gk[k]);
-                    gq[k] = mfma4(q4[r], b4[r], gq[k]);
+                for (int u = 0; u < SD / 16; ++u) {
+                    const f32x4 a4 = ld4(km + 16 * u), q4 = ld4(qm + 16 * u), b4 = ld4(kn + 16 * u);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        gk[k] = mfma4(a4[r], b4[r], gk[k]);
+                        gq[k] = mfma4(q4[r], b4[r], gq[k]);
+                    }
                 }
             }
         }
+
+        bool agent = false;  // this item's stores write through (see above)
+        if constexpr (FUSED) agent = __builtin_amdgcn_readfirstlane(__syncthreads_and(here)) == 0;
 
         if constexpr (SPLIT) {
             // K, Q pieces (token tile m, dim step sg): lane (lr, lq) row 16 m + lr,
@@ -458,7 +483,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             {
                 float l = 0.f, b = 0.f;  // padded tokens: g = 1, b = 0
                 if (lane < nv) {
-                    l = kLog2e * a.ssm_a[hv] * softplus_f(al_n + a.dt_bias[hv]);
+                    l = kLog2e * sa_n * softplus_f(al_n + dtb_n);
                     b = 1.f / (1.f + expf(-be_n));
                 }
                 if (hv + a.n_kh < a.n_vh) ab_fetch(hv + a.n_kh);
@@ -601,6 +626,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0) __hip_atomic_store(flags + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (more) load_rows(item + stride);
         }
     }
 }
@@ -846,10 +872,11 @@ struct ScanLds {
     static constexpr int BYTES = TILES * 8 + 2 * C * KTLD * 2;
 };
 
-// A wait for a ready flag gives up after this many polls (about 2^16 x 2 us
-// at the box's clock), records the failure in *err and lets the workgroup
-// finish, so no launch can hang on a producer that never runs.
-constexpr uint32_t kFlagPolls = 1u << 16;
+// A wait for a ready flag gives up after this many polls (each a memory
+// round trip of a microsecond or more and a short sleep: over a tenth of a
+// second in all), records the failure in *err and lets the workgroup finish,
+// so no launch can hang on a producer that never runs.
+constexpr uint32_t kFlagPolls = 1u << 17;
 
 // blk: the workgroup's (v-head, row block) index.  FUSED: the workgroup
 // first records its XCD at err[1 + blk] (see chunk_prep_body); chunk ch's
@@ -958,7 +985,7 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
                 failed = true;
                 if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            __builtin_amdgcn_s_sleep(32);
+            __builtin_amdgcn_s_sleep(8);
         }
     };
     // Tokens past the end of the last chunk read row 0 of the chunk instead:
@@ -1068,7 +1095,6 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
         if (threadIdx.x == 0) __hip_atomic_store(err + 1 + blk, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_ready(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        in0.rdy = poll(min(1, n_chunks - 1));
     }
     fetch_small(0, in0);
     if (tok_wave) {
@@ -1085,6 +1111,9 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
     }
     put_s();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // FUSED: the next chunk's flag, polled after the drain (an agent-scope
+    // load is a long round trip, which the drain would otherwise wait out)
+    if constexpr (FUSED) in0.rdy = poll(min(1, n_chunks - 1));
     __syncthreads();
     get_s();
     int ch = 0;
@@ -1112,8 +1141,13 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
 // waiting for a chunk's flag before it loads that chunk's inputs.  Prep
 // workgroups never wait and come first in dispatch order, and the host
 // launches this form only when the GPU holds more workgroups than the scan
-// has, so a prep workgroup can always run.  Two workgroups a CU: the scan's
-// chains leave most issue cycles idle, and the prep fills them.
+// has, so a prep workgroup can always run.  Two workgroups a CU (one prep,
+// one scan when all are resident): the scan's chains leave most issue cycles
+// idle, and the prep fills them.  The scan starts once the first chunk's
+// items are done (one item's latency, about 20 us at T = 4096 and 32 v-heads)
+// and slows by a quarter while prep rounds share its CUs; both together cost
+// less than the prep as a launch of its own.  Results are bit-identical to
+// the two-launch form.
 template <int SD, int C>
 __global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, float* ws_T, float* ws_P,
                                                                    float* ws_e, uint8_t* ws_K,
