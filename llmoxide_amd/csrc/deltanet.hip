@@ -1219,12 +1219,16 @@ static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks,
         // One launch when the GPU holds more workgroups than the scan has, so
         // that a prep workgroup can always run.  Prep workgroups: what the GPU
         // holds beside the scan, a multiple of 8 so that scan workgroup j
-        // still runs on XCD j % 8 with the other row blocks of its v-head.
+        // still runs on XCD j % 8 with the other row blocks of its v-head.  A
+        // round of items (one per prep workgroup, about 25 us beside the scan)
+        // yields n_prep / n_kh chunks while the scan takes about ten, so with
+        // fewer than 12 n_kh prep workgroups the scan would wait on the prep
+        // and two launches are faster.
         const int n_scan = n_vh * (SD / 16);
         const int slots = tuning().delta_fused == 0 ? 0 : fused_slots<SD, C>();
-        if (slots > n_scan) {
-            int n_prep = std::min(n_items, slots - n_scan);
-            if (n_prep >= 8) n_prep &= ~7;
+        int n_prep = std::min(n_items, slots - n_scan);
+        if (n_prep >= 8) n_prep &= ~7;
+        if (slots > n_scan && n_prep >= std::min(n_items, 12 * n_kh)) {
             const int n_words = n_items + 1 + n_scan;  // flags, error word, registrations
             hipLaunchKernelGGL(delta_flags_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, st,
                                wsF, n_words);
