@@ -873,10 +873,11 @@ struct ScanLds {
 };
 
 // A wait for a ready flag gives up after this many polls (each a memory
-// round trip of a microsecond or more and a short sleep: over a tenth of a
-// second in all), records the failure in *err and lets the workgroup finish,
-// so no launch can hang on a producer that never runs.
-constexpr uint32_t kFlagPolls = 1u << 17;
+// round trip of a microsecond or more and a short sleep: seconds in all, far
+// beyond any delay a busy GPU imposes on the prep), records the failure in
+// *err and lets the workgroup finish, so no launch can hang on a producer
+// that never runs.
+constexpr uint32_t kFlagPolls = 1u << 21;
 
 // blk: the workgroup's (v-head, row block) index.  FUSED: the workgroup
 // first records its XCD at err[1 + blk] (see chunk_prep_body); chunk ch's

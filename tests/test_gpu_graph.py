@@ -102,10 +102,14 @@ def test_graph_prefill_key_splits():
                  other=lambda: lmx.attention(q * 0.5, k, v, out=out2, **kw), outs=[out])
 
 
-def test_graph_delta_chunked():
-    say("case graph delta chunked T=200 Hv=4 Hk=2 d=128")
+@pytest.mark.parametrize("T,n_vh,n_kh", [(200, 4, 2), (4096, 32, 16)], ids=["small", "c5"])
+def test_graph_delta_chunked(T, n_vh, n_kh):
+    """The chunked delta rule captured and replayed: at C5 size its one-launch
+    form (256 prep beside 256 scan workgroups, after the flag-clearing
+    kernel) runs in the graph."""
+    say(f"case graph delta chunked T={T} Hv={n_vh} Hk={n_kh} d=128")
     g = torch.Generator(device="cuda").manual_seed(6)
-    T, n_vh, n_kh, sd = 200, 4, 2, 128
+    sd = 128
     conv = torch.randn((T, 2 * n_kh * sd + n_vh * sd), generator=g, device="cuda")
     qk = conv[:, :2 * n_kh * sd].view(T, 2 * n_kh, sd)
     qk /= qk.norm(dim=-1, keepdim=True)
