@@ -965,8 +965,22 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
                 kt[jj][sg] = join8(h0, h1, l0, l1);
             }
     };
-    auto ld_tb = [&](int ch, int sg) { tb[sg] = ld_piece(mat_base(ws_T, ch) + (m * SC + sg) * kPiece, lane); };
-    auto ld_mm = [&](int ch, int sg) { mm[sg] = ld_piece(mat_base(ws_P, ch) + (m * SC + sg) * kPiece, lane); };
+    // Tb and M are lower triangular by 16 x 16 blocks: piece (m, sg) covers
+    // blocks 2 sg and 2 sg + 1 of row tile m, all zero when 2 sg > m.  Those
+    // are never loaded (their registers keep the zeros set below), which
+    // spares waves 0 and 1 of chunks of 64 a sixth of their piece bytes.
+    auto tb_live = [&](int sg) { return 2 * sg <= m; };
+    auto ld_tb = [&](int ch, int sg) {
+        if (tb_live(sg)) tb[sg] = ld_piece(mat_base(ws_T, ch) + (m * SC + sg) * kPiece, lane);
+    };
+    auto ld_mm = [&](int ch, int sg) {
+        if (tb_live(sg)) mm[sg] = ld_piece(mat_base(ws_P, ch) + (m * SC + sg) * kPiece, lane);
+    };
+#pragma unroll
+    for (int sg = 0; sg < SC; ++sg) {
+        const bf16x8 zb = {};
+        tb[sg] = mm[sg] = Bf8{zb, zb};
+    }
 
     // Small per-chunk inputs, two register sets (the loop is unrolled by two).
     struct Small {
