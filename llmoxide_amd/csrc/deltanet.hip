@@ -1107,6 +1107,9 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
     // the loop body's own issue order.
     Small in0, in1;
     if constexpr (FUSED) {
+        // The chain first: when a scan wave and a prep wave on one SIMD are
+        // both ready, the scan's instruction issues.
+        __builtin_amdgcn_s_setprio(2);
         if (threadIdx.x == 0) __hip_atomic_store(err + 1 + blk, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_ready(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
