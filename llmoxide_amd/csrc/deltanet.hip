@@ -309,9 +309,11 @@ __device__ __forceinline__ uint32_t xcc_id() {
 //
 // The workgroup walks items first, first + stride, ...  FUSED (inside
 // delta_chunk_fused_kernel): items are numbered chunk-major (chunk ch, k-head
-// hk is item ch n_kh + hk) so that early chunks are done first, and once an
-// item is complete its flag flags[item] is set to 1.  Scan workgroup j records
-// its XCD as reg[j] = XCD + 1 (reg follows the flags and the error word): an
+// hk is item ch n_kh + hk) so that early chunks are done first, and once the
+// factors of v-head hv are out, flags[ch n_vh + hv] is set to 1.  Items below
+// n_split are shared: split_u 0 does v-head u = 0 of the k-head, split_u 1
+// the others (both write the same K/Q pieces).  Scan workgroup j records its
+// XCD as reg[j] = XCD + 1 (reg follows the flags and the error word): an
 // item's stores stay plain only when every scan workgroup that reads them has
 // registered on this workgroup's XCD, and are agent-scope otherwise, so the
 // result never depends on where workgroups run.  Otherwise items are numbered
@@ -320,7 +322,7 @@ template <int SD, int C, bool SPLIT, bool FUSED>
 __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T, float* ws_P,
                                                 float* ws_e, uint8_t* ws_K, int n_chunks,
                                                 int first, int stride, float* lds,
-                                                uint32_t* flags) {
+                                                uint32_t* flags, int n_split, int split_u) {
     constexpr int NM = C / 16, LD = ChunkSmem<C>::LD;
     constexpr int NTILE = NM * (NM + 1) / 2, TPW = (NTILE + 3) / 4;
     constexpr int KLD = PrepLds<SD, C>::KLD;  // staged K/Q row stride in floats
@@ -363,10 +365,14 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
     };
     if (first < n_items) load_rows(first);
     const uint32_t my_xcc = FUSED ? xcc_id() : 0;
-    const uint32_t* const reg = FUSED ? flags + n_items + 1 : nullptr;
+    const uint32_t* const reg = FUSED ? flags + n_chunks * a.n_vh + 1 : nullptr;
+    const int per = a.n_vh / a.n_kh;  // v-heads u = 0 .. per - 1 of a k-head
     for (int item = first; item < n_items; item += stride) {
         const int ch = item_ch(item), hk = item_hk(item);
         const int c0 = ch * C, nv = min(C, a.n_tok - c0);
+        // the v-heads this workgroup does: all, or its share of a shared item
+        const bool shared = FUSED && item < n_split;
+        const int u_lo = shared && split_u > 0 ? 1 : 0, u_hi = shared && split_u == 0 ? 0 : per - 1;
 
         // alpha and beta of the next v-head, in flight during the work before it
         // (and its ssm_a, dt_bias)
@@ -380,7 +386,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
                 be_n = a.beta[gi];
             }
         };
-        ab_fetch(hk);
+        ab_fetch(hk + u_lo * a.n_kh);
 
         // Stage the chunk's K and Q rows (the previous item's LDS reads are done).
         __syncthreads();
@@ -398,9 +404,9 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
         // seen on this XCD here is there for good.
         int here = 1;
         if constexpr (FUSED) {
-            const int per = a.n_vh / a.n_kh, n_rd = per * (SD / 16);
+            const int nu = u_hi - u_lo + 1, n_rd = nu * (SD / 16);
             for (int r = tid; r < n_rd; r += 256) {
-                const int hv = hk + (r % per) * a.n_kh, rb = r / per;
+                const int hv = hk + (u_lo + r % nu) * a.n_kh, rb = r / nu;
                 here &= __hip_atomic_load(reg + rb * a.n_vh + hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                         my_xcc + 1;
             }
@@ -475,7 +481,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             }
         }
 
-        for (int hv = hk; hv < a.n_vh; hv += a.n_kh) {
+        for (int hv = hk + u_lo * a.n_kh; hv <= hk + u_hi * a.n_kh; hv += a.n_kh) {
             const size_t cb = (size_t)hv * n_chunks + ch;
             // the staging (first head) or the previous head's A, T, P are no longer read
             __syncthreads();
@@ -486,7 +492,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
                     l = kLog2e * sa_n * softplus_f(al_n + dtb_n);
                     b = 1.f / (1.f + expf(-be_n));
                 }
-                if (hv + a.n_kh < a.n_vh) ab_fetch(hv + a.n_kh);
+                if (hv + a.n_kh <= hk + u_hi * a.n_kh) ab_fetch(hv + a.n_kh);
 #pragma unroll
                 for (int off = 1; off < 64; off <<= 1) {
                     const float y = __shfl_up(l, off);
@@ -625,7 +631,9 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             // Every thread's stores of the item acknowledged, then the flag.
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            if (tid == 0) __hip_atomic_store(flags + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid <= u_hi - u_lo)
+                __hip_atomic_store(flags + ch * a.n_vh + hk + (u_lo + tid) * a.n_kh, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             if (more) load_rows(item + stride);
         }
     }
@@ -637,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_prep_kernel(DeltaArgs a, f
                                                                uint8_t* ws_K, int n_chunks) {
     __shared__ __attribute__((aligned(16))) float lds[PrepLds<SD, C>::FLOATS];
     chunk_prep_body<SD, C, SPLIT, false>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, blockIdx.x, gridDim.x,
-                                         lds, nullptr);
+                                         lds, nullptr, 0, 0);
 }
 
 // One workgroup per (v-head, 16 state rows); blockIdx % n_vh == hv, so with
@@ -879,11 +887,10 @@ struct ScanLds {
 // that never runs.
 constexpr uint32_t kFlagPolls = 1u << 21;
 
-// blk: the workgroup's (v-head, row block) index.  FUSED: the workgroup
-// first records its XCD at err[1 + blk] (see chunk_prep_body); chunk ch's
-// inputs of its k-head are ready once flags[ch n_kh + hk] is 1, and the flag
-// of the chunk after next is polled a chunk ahead, so a producer that keeps
-// ahead costs no round trip on the chain.
+// blk: the workgroup's (v-head, row block) index.  FUSED: chunk ch's inputs
+// of its v-head are ready once flags[ch n_vh + hv] is 1, and the flag of the
+// chunk after next is polled a chunk ahead, so a producer that keeps ahead
+// costs no round trip on the chain.
 template <int SD, int C, bool FUSED>
 __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uint8_t* ws_T,
                                                    const uint8_t* ws_P, const float* ws_e,
@@ -992,7 +999,7 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
     // workgroup waits no more).
     bool failed = false;
     auto poll = [&](int c) -> uint32_t {
-        return __hip_atomic_load(flags + (size_t)c * a.n_kh + hk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return __hip_atomic_load(flags + (size_t)c * a.n_vh + hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     auto wait_ready = [&](int c) {
         for (uint32_t n = 0; !failed && __builtin_amdgcn_readfirstlane(poll(c)) == 0; ++n) {
@@ -1110,7 +1117,6 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
         // The chain first: when a scan wave and a prep wave on one SIMD are
         // both ready, the scan's instruction issues.
         __builtin_amdgcn_s_setprio(2);
-        if (threadIdx.x == 0) __hip_atomic_store(err + 1 + blk, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_ready(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
@@ -1155,8 +1161,12 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
 
 // Prep and scan in one launch (chunks of 32 and 64).  Workgroups [0, n_prep)
 // run the prep over items b, b + n_prep, ... in chunk order and publish each
-// item's flag; workgroups [n_prep, n_prep + n_vh SD / 16) run the scan, each
-// waiting for a chunk's flag before it loads that chunk's inputs.  Prep
+// v-head's flag; workgroups [n_prep, n_prep + n_vh SD / 16) run the scan, each
+// waiting for a chunk's flag before it loads that chunk's inputs.  The first
+// n_split items (the first round, which the scan waits for) are shared: prep
+// workgroup j does v-head 0 of item j and scan workgroup j, idle until then,
+// the other v-heads before its scan, which shortens the first chunk's wait by
+// a v-head's solve and products.  Prep
 // workgroups never wait and come first in dispatch order, and the host
 // launches this form only when the GPU holds more workgroups than the scan
 // has, so a prep workgroup can always run.  Two workgroups a CU (one prep,
@@ -1169,18 +1179,26 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
 template <int SD, int C>
 __global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, float* ws_T, float* ws_P,
                                                                    float* ws_e, uint8_t* ws_K,
-                                                                   int n_chunks, int n_prep,
+                                                                   int n_chunks, int n_prep, int n_split,
                                                                    uint32_t* flags, uint32_t* err) {
     constexpr int PB = PrepLds<SD, C>::FLOATS * 4, SB = ScanLds<SD, C>::BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t lds[PB > SB ? PB : SB];
     const int b = blockIdx.x;
-    if (b < n_prep)
+    if (b < n_prep) {
         chunk_prep_body<SD, C, true, true>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, b, n_prep,
-                                           reinterpret_cast<float*>(lds), flags);
-    else
+                                           reinterpret_cast<float*>(lds), flags, n_split, 0);
+    } else {
+        const int j = b - n_prep;
+        if (threadIdx.x == 0) __hip_atomic_store(err + 1 + j, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (j < n_split) {
+            chunk_prep_body<SD, C, true, true>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, j, n_chunks * a.n_kh,
+                                               reinterpret_cast<float*>(lds), flags, n_split, 1);
+            __syncthreads();  // the scan reuses the LDS
+        }
         chunk_scan_bf_body<SD, C, true>(a, reinterpret_cast<const uint8_t*>(ws_T),
-                                        reinterpret_cast<const uint8_t*>(ws_P), ws_e, ws_K, n_chunks,
-                                        b - n_prep, lds, flags, err);
+                                        reinterpret_cast<const uint8_t*>(ws_P), ws_e, ws_K, n_chunks, j, lds,
+                                        flags, err);
+    }
 }
 
 // Clears the one-launch form's flags, error word and registrations (a kernel,
@@ -1193,7 +1211,7 @@ __global__ __launch_bounds__(256) void delta_flags_clear_kernel(uint32_t* p, int
 // split-bf16 pieces of the same size), the decays [n_vh][n_chunks][2 chunk],
 // and, for the split path (chunks of 32 and 64), K and Q pieces
 // [n_chunks][n_kh][2 chunk s_dim] floats' worth, then the one-launch form's
-// ready flags [n_chunks][n_kh], its error word and the scan workgroups' XCD
+// ready flags [n_chunks][n_vh], its error word and the scan workgroups' XCD
 // registrations [n_vh s_dim / 16].
 static bool chunk_split(int chunk) { return chunk >= 32; }
 
@@ -1201,7 +1219,7 @@ static size_t chunk_ws_floats(const lmx_dop* op, int chunk) {
     const size_t n_chunks = (op->n_tok + chunk - 1) / chunk;
     const bool split = chunk_split(chunk);
     const size_t kq = split ? (size_t)op->n_kh * n_chunks * 2 * chunk * op->s_dim : 0;
-    const size_t fl = split ? (size_t)op->n_kh * n_chunks + 1 + (size_t)op->n_vh * (op->s_dim / 16) : 0;
+    const size_t fl = split ? (size_t)op->n_vh * n_chunks + 1 + (size_t)op->n_vh * (op->s_dim / 16) : 0;
     return (size_t)op->n_vh * n_chunks * ((size_t)2 * chunk * chunk + 2 * chunk) + kq + fl;
 }
 
@@ -1247,11 +1265,15 @@ static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks,
         int n_prep = std::min(n_items, slots - n_scan);
         if (n_prep >= 8) n_prep &= ~7;
         if (slots > n_scan && n_prep >= std::min(n_items, 12 * n_kh)) {
-            const int n_words = n_items + 1 + n_scan;  // flags, error word, registrations
+            const int n_flags = n_chunks * n_vh;
+            const int n_words = n_flags + 1 + n_scan;  // flags, error word, registrations
+            // the first round's items are shared with the scan workgroups when
+            // a k-head has several v-heads
+            const int n_split = n_vh > n_kh ? std::min(n_prep, std::min(n_scan, n_items)) : 0;
             hipLaunchKernelGGL(delta_flags_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, st,
                                wsF, n_words);
             hipLaunchKernelGGL((delta_chunk_fused_kernel<SD, C>), dim3(n_prep + n_scan), dim3(256), 0, st, a,
-                               wsT, wsP, wsE, wsK, n_chunks, n_prep, wsF, wsF + n_items);
+                               wsT, wsP, wsE, wsK, n_chunks, n_prep, n_split, wsF, wsF + n_flags);
             return;
         }
     }

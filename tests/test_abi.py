@@ -195,7 +195,7 @@ def test_deltanet_chunked_workspace_size(T, n_vh, n_kh, sd):
     # per (v-head, chunk): Tb and M (chunk^2 floats each) and the decays (2 chunk);
     # chunks of 32 and 64 add the split-bf16 K and Q of every (chunk, k-head),
     # 2 * chunk * s_dim floats' worth, and the one-launch form's ready flag of
-    # every (chunk, k-head), its error word and one word per scan workgroup
+    # every (chunk, v-head), its error word and one word per scan workgroup
     # (n_vh * s_dim / 16); all rounded up to 256 bytes
     L = lmx.lib()
     op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
@@ -203,7 +203,7 @@ def test_deltanet_chunked_workspace_size(T, n_vh, n_kh, sd):
         n_ch = (T + chunk - 1) // chunk
         floats = n_vh * n_ch * (2 * chunk * chunk + 2 * chunk)
         if chunk >= 32:
-            floats += n_kh * n_ch * 2 * chunk * sd + n_kh * n_ch + 1 + n_vh * sd // 16
+            floats += n_kh * n_ch * 2 * chunk * sd + n_vh * n_ch + 1 + n_vh * sd // 16
         want = (floats * 4 + 255) // 256 * 256
         assert L.lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk) == want
 

@@ -162,7 +162,7 @@ def test_delta_chunked_c5_full_size_matches_sequential_kernel():
                                                   (37, 4, 2, 64, 64)])
 def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_env):
     """The one-launch form (prep workgroups publish a ready flag per (chunk,
-    k-head); scan workgroups wait for it) against prep and scan as two
+    v-head); scan workgroups wait for it) against prep and scan as two
     launches (LMX_DELTA_FUSED=0).  Each item and chunk runs the same
     arithmetic, so o and the state are bit-identical.  The workspace is
     filled with 0x5A bytes before each call, so its flags start nonzero: the
@@ -171,7 +171,7 @@ def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_e
     say(f"delta_chunked one launch vs two T={T} n_vh={n_vh} n_kh={n_kh} sd={sd} chunk={chunk}")
     conv, al, be, S0, A, dt = delta_inputs(T + 5, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.1)
     n_ch = -(-T // chunk)
-    err_at = 4 * (n_vh * n_ch * (2 * chunk * chunk + 2 * chunk) + n_kh * n_ch * 2 * chunk * sd + n_kh * n_ch)
+    err_at = 4 * (n_vh * n_ch * (2 * chunk * chunk + 2 * chunk) + n_kh * n_ch * 2 * chunk * sd + n_vh * n_ch)
     op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
     ws = lmx.Workspace(lmx.lib().lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk),
                        device=torch.device("cuda"))
