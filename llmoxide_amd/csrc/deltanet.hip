@@ -412,9 +412,9 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
             }
         }
         // The next item's rows.  FUSED issues them once this item is
-        // published: beside the scan, issuing them stalls the wave for microseconds,
-        // and an item's latency matters only for the first chunks, which the
-        // scan waits for; later items have time to spare.
+        // published: beside the scan, issuing them stalls the wave for
+        // microseconds, and an item's latency matters most for the first
+        // chunks, which the scan waits for; later rounds run ahead of it.
         const bool more = item + stride < n_items;
         if (!FUSED && more) load_rows(item + stride);
 
