@@ -1253,9 +1253,11 @@ static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks,
     const int n_items = n_chunks * n_kh;
     if constexpr (SPLIT) {
         // One launch when the GPU holds more workgroups than the scan has, so
-        // that a prep workgroup can always run.  Prep workgroups: what the GPU
-        // holds beside the scan, a multiple of 8 so that scan workgroup j
-        // still runs on XCD j % 8 with the other row blocks of its v-head.  A
+        // that a prep workgroup can always run.  Prep workgroups: one per item,
+        // at most what the GPU holds beside the scan, rounded up to a multiple
+        // of 8 where that fits (the extra ones have no item and exit) so that
+        // scan workgroup j still runs on XCD j % 8 with the other row blocks
+        // of its v-head.  A
         // round of items (one per prep workgroup, about 25 us beside the scan)
         // yields n_prep / n_kh chunks while the scan takes about ten, so with
         // fewer than 12 n_kh prep workgroups the scan would wait on the prep
@@ -1263,7 +1265,7 @@ static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks,
         const int n_scan = n_vh * (SD / 16);
         const int slots = tuning().delta_fused == 0 ? 0 : fused_slots<SD, C>();
         int n_prep = std::min(n_items, slots - n_scan);
-        if (n_prep >= 8) n_prep &= ~7;
+        n_prep = std::min((n_prep + 7) & ~7, slots - n_scan);
         if (slots > n_scan && n_prep >= std::min(n_items, 12 * n_kh)) {
             const int n_flags = n_chunks * n_vh;
             const int n_words = n_flags + 1 + n_scan;  // flags, error word, registrations

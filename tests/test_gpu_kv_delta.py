@@ -97,6 +97,21 @@ def test_delta_chunked_matches_sequential(T, chunk):
     assert_close(S, S_ref, what="S")
 
 
+@pytest.mark.parametrize("n_vh,n_kh,T,chunk", [(4, 4, 150, 64), (12, 3, 99, 32), (8, 2, 150, 64)],
+                         ids=["one_v_head_a_k_head", "three", "four"])
+def test_delta_chunked_head_ratios(n_vh, n_kh, T, chunk):
+    """v-heads per k-head other than two: with one, the one-launch form shares
+    no item with the scan workgroups; with three or four, a scan workgroup's
+    share of a first-round item is several v-heads, each with its own flag."""
+    sd = 128
+    say(f"delta_chunked n_vh={n_vh} n_kh={n_kh} T={T} chunk={chunk}")
+    conv, al, be, S0, A, dt = delta_inputs(T + n_vh, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.2)
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    o, S = _delta_gpu(lmx.delta_chunked, conv, al, be, S0, A, dt, n_vh, n_kh, sd, chunk=chunk)
+    assert_close(o, o_ref, what="o")
+    assert_close(S, S_ref, what="S")
+
+
 # ------------------------------------------------------- ragged batch decode --
 def _batched(B, lens, H=32, Hkv=8, hd=128, seed=0, q_f16=False):
     say(f"batched B={B} lens={lens}")
@@ -159,7 +174,8 @@ def test_delta_chunked_c5_full_size_matches_sequential_kernel():
 
 @pytest.mark.parametrize("T,n_vh,n_kh,sd,chunk", [(4096, 32, 16, 128, 64), (2577, 32, 16, 128, 64),
                                                   (250, 8, 4, 64, 32), (99, 4, 2, 128, 32),
-                                                  (37, 4, 2, 64, 64)])
+                                                  (37, 4, 2, 64, 64), (150, 4, 4, 128, 64),
+                                                  (99, 12, 3, 128, 32), (150, 8, 2, 128, 64)])
 def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_env):
     """The one-launch form (prep workgroups publish a ready flag per (chunk,
     v-head); scan workgroups wait for it) against prep and scan as two
