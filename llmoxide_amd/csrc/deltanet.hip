@@ -1191,6 +1191,9 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, 
         const int j = b - n_prep;
         if (threadIdx.x == 0) __hip_atomic_store(err + 1 + j, xcc_id() + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (j < n_split) {
+            // Above the prep workgroup sharing this CU, whose waves are older
+            // and would otherwise issue first: the first chunk needs both halves.
+            __builtin_amdgcn_s_setprio(1);
             chunk_prep_body<SD, C, true, true>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, j, n_chunks * a.n_kh,
                                                reinterpret_cast<float*>(lds), flags, n_split, 1);
             __syncthreads();  // the scan reuses the LDS
