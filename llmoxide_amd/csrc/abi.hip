@@ -199,8 +199,7 @@ static void read_tuning_env() {
     g_tune_krows.store(choice("LMX_DECODE_KROWS", "1", 1, "0", 0));
     const char* mh = std::getenv("LMX_DECODE_MH");
     g_tune_mh.store(mh && mh[0] == '0' ? 0 : -1);
-    const char* df = std::getenv("LMX_DELTA_FUSED");
-    g_tune_dfused.store(df && df[0] == '0' ? 0 : -1);
+    g_tune_dfused.store(choice("LMX_DELTA_FUSED", "0", 0, "starve", 2));
 }
 
 Tuning tuning() {

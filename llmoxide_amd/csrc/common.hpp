@@ -79,7 +79,7 @@ __device__ __forceinline__ f32x4 gate_sigmoid4(f32x4 o, const float* g) {
 
 // Kernel-choice overrides for tests and tuning sweeps, from the environment
 // (LMX_PREFILL_KERNEL = pp | tile, LMX_PREFILL_GP = 1 | 2 | 4,
-// LMX_PREFILL_KH = 0, LMX_DECODE_KROWS = 0 | 1, LMX_DECODE_MH = 0, LMX_DELTA_FUSED = 0).
+// LMX_PREFILL_KH = 0, LMX_DECODE_KROWS = 0 | 1, LMX_DECODE_MH = 0, LMX_DELTA_FUSED = 0 | starve).
 // Read once, at the first
 // launch, and again only by lmx_tuning_reload(): no getenv on the launch path,
 // so a launch and the workspace-size query it was sized by see the same
@@ -90,7 +90,9 @@ struct Tuning {
     int prefill_kh;      // 0: key halves off
     int decode_krows;    // K rows through LDS (1) or direct operand loads (0)
     int decode_mh;       // 0: head_dim 512 keeps attn_decode_kernel even for 16 heads a kv head
-    int delta_fused;     // 0: the chunked delta rule runs prep and scan as two launches
+    int delta_fused;     // 0: the chunked delta rule runs prep and scan as two launches;
+                         // 2 (tests only): one launch with no prep workgroups and a
+                         // 64-poll wait bound, so every flag wait gives up
 };
 Tuning tuning();  // the current overrides (abi.hip)
 

@@ -884,7 +884,7 @@ struct ScanLds {
 // round trip of a microsecond or more and a short sleep: seconds in all, far
 // beyond any delay a busy GPU imposes on the prep), records the failure in
 // *err and lets the workgroup finish, so no launch can hang on a producer
-// that never runs.
+// that never runs.  (A test launches with no prep and a bound of 64.)
 constexpr uint32_t kFlagPolls = 1u << 21;
 
 // blk: the workgroup's (v-head, row block) index.  FUSED: chunk ch's inputs
@@ -896,7 +896,7 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
                                                    const uint8_t* ws_P, const float* ws_e,
                                                    const uint8_t* ws_K, int n_chunks, int blk,
                                                    uint8_t* lds, const uint32_t* flags,
-                                                   uint32_t* err) {
+                                                   uint32_t* err, uint32_t max_polls) {
     constexpr int NT = SD / 16, NM = C / 16, TPW = NT / 4;
     constexpr int SX = SD / 32, SC = C / 32;  // 32-wide steps over dims, over tokens
     constexpr size_t KQB = (size_t)2 * C * SD * 4;  // ws_K bytes per (chunk, k-head)
@@ -1003,7 +1003,7 @@ __device__ __forceinline__ void chunk_scan_bf_body(const DeltaArgs& a, const uin
     };
     auto wait_ready = [&](int c) {
         for (uint32_t n = 0; !failed && __builtin_amdgcn_readfirstlane(poll(c)) == 0; ++n) {
-            if (n == kFlagPolls) {
+            if (n == max_polls) {
                 failed = true;
                 if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -1156,7 +1156,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_bf_kernel(DeltaArgs a, c
                                                                   const float* ws_e,
                                                                   const uint8_t* ws_K, int n_chunks) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[ScanLds<SD, C>::BYTES];
-    chunk_scan_bf_body<SD, C, false>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, blockIdx.x, lds, nullptr, nullptr);
+    chunk_scan_bf_body<SD, C, false>(a, ws_T, ws_P, ws_e, ws_K, n_chunks, blockIdx.x, lds, nullptr, nullptr, 0);
 }
 
 // Prep and scan in one launch (chunks of 32 and 64).  Workgroups [0, n_prep)
@@ -1180,7 +1180,8 @@ template <int SD, int C>
 __global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, float* ws_T, float* ws_P,
                                                                    float* ws_e, uint8_t* ws_K,
                                                                    int n_chunks, int n_prep, int n_split,
-                                                                   uint32_t* flags, uint32_t* err) {
+                                                                   uint32_t* flags, uint32_t* err,
+                                                                   uint32_t max_polls) {
     constexpr int PB = PrepLds<SD, C>::FLOATS * 4, SB = ScanLds<SD, C>::BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t lds[PB > SB ? PB : SB];
     const int b = blockIdx.x;
@@ -1200,7 +1201,7 @@ __global__ __launch_bounds__(256, 2) void delta_chunk_fused_kernel(DeltaArgs a, 
         }
         chunk_scan_bf_body<SD, C, true>(a, reinterpret_cast<const uint8_t*>(ws_T),
                                         reinterpret_cast<const uint8_t*>(ws_P), ws_e, ws_K, n_chunks, j, lds,
-                                        flags, err);
+                                        flags, err, max_polls);
     }
 }
 
@@ -1266,19 +1267,23 @@ static void launch_chunked(const DeltaArgs& a, int n_vh, int n_kh, int n_chunks,
         // fewer than 12 n_kh prep workgroups the scan would wait on the prep
         // and two launches are faster.
         const int n_scan = n_vh * (SD / 16);
-        const int slots = tuning().delta_fused == 0 ? 0 : fused_slots<SD, C>();
+        const int mode = tuning().delta_fused;
+        const int slots = mode == 0 ? 0 : fused_slots<SD, C>();
         int n_prep = std::min(n_items, slots - n_scan);
         n_prep = std::min((n_prep + 7) & ~7, slots - n_scan);
-        if (slots > n_scan && n_prep >= std::min(n_items, 12 * n_kh)) {
+        const bool starve = mode == 2;  // tests only: no prep, so every wait gives up
+        if (starve) n_prep = 0;
+        if (starve || (slots > n_scan && n_prep >= std::min(n_items, 12 * n_kh))) {
             const int n_flags = n_chunks * n_vh;
             const int n_words = n_flags + 1 + n_scan;  // flags, error word, registrations
             // the first round's items are shared with the scan workgroups when
             // a k-head has several v-heads
             const int n_split = n_vh > n_kh ? std::min(n_prep, std::min(n_scan, n_items)) : 0;
+            const uint32_t max_polls = starve ? 64u : kFlagPolls;
             hipLaunchKernelGGL(delta_flags_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, st,
                                wsF, n_words);
             hipLaunchKernelGGL((delta_chunk_fused_kernel<SD, C>), dim3(n_prep + n_scan), dim3(256), 0, st, a,
-                               wsT, wsP, wsE, wsK, n_chunks, n_prep, n_split, wsF, wsF + n_flags);
+                               wsT, wsP, wsE, wsK, n_chunks, n_prep, n_split, wsF, wsF + n_flags, max_polls);
             return;
         }
     }

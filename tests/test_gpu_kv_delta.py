@@ -208,6 +208,40 @@ def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_e
     np.testing.assert_array_equal(runs["1"][1], runs["0"][1])
 
 
+def test_delta_chunked_flag_wait_gives_up(tuning_env):
+    """The one-launch form's waits are bounded.  LMX_DELTA_FUSED=starve (tests
+    only) launches it with no prep workgroups and a 64-poll bound: every scan
+    workgroup's first wait gives up, records it in the error word and lets the
+    workgroup finish, so the call returns (its results are meaningless).  A
+    normal call on the same workspace afterwards is correct again."""
+    T, n_vh, n_kh, sd, chunk = 200, 4, 2, 128, 64
+    say("delta_chunked flag wait gives up (no prep workgroups)")
+    conv, al, be, S0, A, dt = delta_inputs(T + 9, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.1)
+    n_ch = -(-T // chunk)
+    err_at = 4 * (n_vh * n_ch * (2 * chunk * chunk + 2 * chunk) + n_kh * n_ch * 2 * chunk * sd + n_vh * n_ch)
+    op = lmx.dop(n_tok=T, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    ws = lmx.Workspace(lmx.lib().lmx_deltanet_chunked_workspace_bytes(ctypes.byref(op), chunk),
+                       device=torch.device("cuda"))
+    base = ws.base - ws.buf.data_ptr()
+
+    def run():
+        state = dev(S0.copy())
+        out = lmx.delta_chunked(dev(conv), dev(al), dev(be), state, dev(A), dev(dt), n_vh=n_vh, n_kh=n_kh,
+                                s_dim=sd, chunk=chunk, workspace=ws)
+        torch.cuda.synchronize()
+        err = int(ws.buf[base + err_at:base + err_at + 4].cpu().numpy().view(np.uint32)[0])
+        return out.cpu().numpy(), state.cpu().numpy(), err
+
+    tuning_env("LMX_DELTA_FUSED", "starve")
+    assert run()[2] == 1
+    tuning_env("LMX_DELTA_FUSED", "1")
+    o, S, err = run()
+    assert err == 0
+    o_ref, S_ref = oracle.delta_recur(conv, al, be, S0, n_vh=n_vh, n_kh=n_kh, s_dim=sd)
+    assert_close(o, o_ref, what="o")
+    assert_close(S, S_ref, what="S")
+
+
 @pytest.mark.parametrize("T", [2577, 6400])
 def test_delta_chunked_prep_items_per_workgroup(T):
     """The chunk prep walks (chunk, k-head) items with a stride of its grid
