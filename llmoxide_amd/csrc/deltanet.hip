@@ -366,13 +366,14 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
     if (first < n_items) load_rows(first);
     const uint32_t my_xcc = FUSED ? xcc_id() : 0;
     const uint32_t* const reg = FUSED ? flags + n_chunks * a.n_vh + 1 : nullptr;
-    const int per = a.n_vh / a.n_kh;  // v-heads u = 0 .. per - 1 of a k-head
     for (int item = first; item < n_items; item += stride) {
         const int ch = item_ch(item), hk = item_hk(item);
         const int c0 = ch * C, nv = min(C, a.n_tok - c0);
-        // the v-heads this workgroup does: all, or its share of a shared item
+        // the v-heads hk + u n_kh (u = 0 .. u_last; n_vh need not be a multiple
+        // of n_kh) this workgroup does: all, or its share of a shared item
+        const int u_last = (a.n_vh - 1 - hk) / a.n_kh;
         const bool shared = FUSED && item < n_split;
-        const int u_lo = shared && split_u > 0 ? 1 : 0, u_hi = shared && split_u == 0 ? 0 : per - 1;
+        const int u_lo = shared && split_u > 0 ? 1 : 0, u_hi = shared && split_u == 0 ? 0 : u_last;
 
         // alpha and beta of the next v-head, in flight during the work before it
         // (and its ssm_a, dt_bias)

@@ -97,12 +97,15 @@ def test_delta_chunked_matches_sequential(T, chunk):
     assert_close(S, S_ref, what="S")
 
 
-@pytest.mark.parametrize("n_vh,n_kh,T,chunk", [(4, 4, 150, 64), (12, 3, 99, 32), (8, 2, 150, 64)],
-                         ids=["one_v_head_a_k_head", "three", "four"])
+@pytest.mark.parametrize("n_vh,n_kh,T,chunk", [(4, 4, 150, 64), (12, 3, 99, 32), (8, 2, 150, 64),
+                                                (6, 4, 150, 64)],
+                         ids=["one_v_head_a_k_head", "three", "four", "uneven"])
 def test_delta_chunked_head_ratios(n_vh, n_kh, T, chunk):
     """v-heads per k-head other than two: with one, the one-launch form shares
     no item with the scan workgroups; with three or four, a scan workgroup's
-    share of a first-round item is several v-heads, each with its own flag."""
+    share of a first-round item is several v-heads, each with its own flag;
+    uneven (6 on 4: k-heads 0 and 1 serve two, 2 and 3 one), some scan
+    workgroups' share is empty."""
     sd = 128
     say(f"delta_chunked n_vh={n_vh} n_kh={n_kh} T={T} chunk={chunk}")
     conv, al, be, S0, A, dt = delta_inputs(T + n_vh, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.2)
@@ -175,7 +178,8 @@ def test_delta_chunked_c5_full_size_matches_sequential_kernel():
 @pytest.mark.parametrize("T,n_vh,n_kh,sd,chunk", [(4096, 32, 16, 128, 64), (2577, 32, 16, 128, 64),
                                                   (250, 8, 4, 64, 32), (99, 4, 2, 128, 32),
                                                   (37, 4, 2, 64, 64), (150, 4, 4, 128, 64),
-                                                  (99, 12, 3, 128, 32), (150, 8, 2, 128, 64)])
+                                                  (99, 12, 3, 128, 32), (150, 8, 2, 128, 64),
+                                                  (150, 6, 4, 128, 64)])
 def test_delta_chunked_one_launch_matches_two(T, n_vh, n_kh, sd, chunk, tuning_env):
     """The one-launch form (prep workgroups publish a ready flag per (chunk,
     v-head); scan workgroups wait for it) against prep and scan as two
