@@ -371,9 +371,11 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
         const int c0 = ch * C, nv = min(C, a.n_tok - c0);
         // the v-heads hk + u n_kh (u = 0 .. u_last; n_vh need not be a multiple
         // of n_kh) this workgroup does: all, or its share of a shared item
-        const int u_last = (a.n_vh - 1 - hk) / a.n_kh;
+        // (none, u_last = -1, for a k-head past the v-heads)
+        const int u_last = hk < a.n_vh ? (a.n_vh - 1 - hk) / a.n_kh : -1;
         const bool shared = FUSED && item < n_split;
-        const int u_lo = shared && split_u > 0 ? 1 : 0, u_hi = shared && split_u == 0 ? 0 : u_last;
+        const int u_lo = shared && split_u > 0 ? 1 : 0;
+        const int u_hi = shared && split_u == 0 ? min(0, u_last) : u_last;
 
         // alpha and beta of the next v-head, in flight during the work before it
         // (and its ssm_a, dt_bias)
@@ -387,7 +389,7 @@ __device__ __forceinline__ void chunk_prep_body(const DeltaArgs& a, float* ws_T,
                 be_n = a.beta[gi];
             }
         };
-        ab_fetch(hk + u_lo * a.n_kh);
+        if (u_lo <= u_hi) ab_fetch(hk + u_lo * a.n_kh);
 
         // Stage the chunk's K and Q rows (the previous item's LDS reads are done).
         __syncthreads();

@@ -98,14 +98,15 @@ def test_delta_chunked_matches_sequential(T, chunk):
 
 
 @pytest.mark.parametrize("n_vh,n_kh,T,chunk", [(4, 4, 150, 64), (12, 3, 99, 32), (8, 2, 150, 64),
-                                                (6, 4, 150, 64)],
-                         ids=["one_v_head_a_k_head", "three", "four", "uneven"])
+                                                (6, 4, 150, 64), (2, 4, 150, 64)],
+                         ids=["one_v_head_a_k_head", "three", "four", "uneven", "more_k_heads"])
 def test_delta_chunked_head_ratios(n_vh, n_kh, T, chunk):
     """v-heads per k-head other than two: with one, the one-launch form shares
     no item with the scan workgroups; with three or four, a scan workgroup's
     share of a first-round item is several v-heads, each with its own flag;
     uneven (6 on 4: k-heads 0 and 1 serve two, 2 and 3 one), some scan
-    workgroups' share is empty."""
+    workgroups' share is empty; with more k-heads than v-heads, k-heads 2 and 3
+    serve none."""
     sd = 128
     say(f"delta_chunked n_vh={n_vh} n_kh={n_kh} T={T} chunk={chunk}")
     conv, al, be, S0, A, dt = delta_inputs(T + n_vh, T=T, n_vh=n_vh, n_kh=n_kh, sd=sd, s0_scale=0.2)
