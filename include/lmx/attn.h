@@ -302,7 +302,10 @@ lmx_status lmx_deltanet_recur(const lmx_dop *op, const float *ssm_a, const float
  * head, deltanet.wgsl:175-239), so this is the prefill counterpart of the same
  * dispatch.  chunk: 64 (or 32, 16).  Chunks of 32 and 64 form their products
  * on bf16 matrix cores from split (hi + lo) operands with fp32 accumulation
- * (about 1e-5 relative to fp32 products); the state stays fp32.
+ * (about 1e-5 relative to fp32 products); the state stays fp32.  They run as
+ * a small flag-clearing kernel and one kernel in which the per-chunk factors
+ * are built beside the chunk chain (as two kernels when the GPU would not hold
+ * enough workgroups for both); the results are bit-identical either way.
  */
 size_t lmx_deltanet_chunked_workspace_bytes(const lmx_dop *op, int32_t chunk);
 
