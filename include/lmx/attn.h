@@ -99,8 +99,8 @@ const char *lmx_status_str(lmx_status s);
 int lmx_version(void);
 
 /* Kernel-choice overrides (LMX_PREFILL_KERNEL, LMX_PREFILL_GP, LMX_PREFILL_KH,
- * LMX_DECODE_KROWS, LMX_DECODE_MH) are read from the environment once, at the
- * first launch.
+ * LMX_DECODE_KROWS, LMX_DECODE_MH, LMX_DELTA_FUSED) are read from the
+ * environment once, at the first launch.
  * This reads them again, for tests and tuning sweeps.  No reference
  * counterpart.  Not to be called while another thread launches. */
 void lmx_tuning_reload(void);
